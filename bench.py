@@ -1,0 +1,304 @@
+#!/usr/bin/env python3
+"""Benchmark of libllmk's non-GEMM layer kernels on one MI355X.
+
+Headline (the JSON line's `value`): the fused residual add + RMSNorm over [8192, 2048] fp16
+-- whole-job throughput in GB/s of algorithmic bytes (inputs read once,
+outputs written once), inputs resident in HBM before the timed region. One step = one launch
+over the full batch. The other BASELINE configurations (RMSNorm [16,2048], RoPE, SwiGLU,
+embedding gather, the 16-layer decode-step pass captured in a HIP graph) and a copy probe are
+measured the same way and reported under "kernels".
+
+Caches: MI355X has a 256 MB Infinity Cache (MALL) in front of HBM and 4 MB of L2 per XCD. Each
+kernel cycles through enough independent input sets that the data of a launch was last
+touched more than 1 GB of traffic earlier, so it cannot be served from the MALL.
+
+Timing: every launch is bracketed by HIP events recorded on the stream it is launched on
+(torch's current stream); `roofline.achieved` = algorithmic bytes / mean event time of one
+launch. `ms_per_step` = wall time of the K timed steps (synchronised on both sides) / K.
+
+CPU baseline: the scalar C oracle of the same op (oracle/, test infrastructure) on the host's
+cores, over a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--kernels all|headline] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = ("achieved HBM GB/s (% of ~8 TB/s) per fused kernel; "
+          "µs per 16-layer non-GEMM pass")
+PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_counters.txt")
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--kernels", choices=["all", "headline"], default="all")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def read_traffic() -> dict:
+    """Counter-based HBM bytes per launch, from the committed rocprofv3 summary (one line per
+    kernel: `<name> traffic_bytes=<int> ...`)."""
+    out = {}
+    if os.path.exists(TRAFFIC_FILE):
+        for line in open(TRAFFIC_FILE):
+            parts = line.split()
+            if len(parts) >= 2 and not line.startswith("#"):
+                kv = dict(p.split("=", 1) for p in parts[1:] if "=" in p)
+                if "traffic_bytes" in kv:
+                    out[parts[0]] = int(float(kv["traffic_bytes"]))
+    return out
+
+
+class Timer:
+    """Per-launch HIP events on the launching stream plus host wall time over the region."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, launch, n_sets: int, steps: int, warmup: int):
+        torch = self.torch
+        for i in range(warmup):
+            launch(i % n_sets)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            ev[i][0].record(stream)
+            launch((warmup + i) % n_sets)
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = [a.elapsed_time(b) * 1e-3 for a, b in ev]  # seconds
+        per.sort()
+        return {"wall_s": wall, "mean_s": sum(per) / len(per), "median_s": per[len(per) // 2],
+                "min_s": per[0]}
+
+
+def kernel_entry(name, nbytes, t, traffic=None, extra=None):
+    achieved = nbytes / t["mean_s"] / 1e9
+    e = {"bytes": nbytes, "us_mean": round(t["mean_s"] * 1e6, 3),
+         "us_median": round(t["median_s"] * 1e6, 3), "us_min": round(t["min_s"] * 1e6, 3),
+         "GBps": round(achieved, 1), "frac_of_peak": round(achieved / PEAK_GBS, 4)}
+    if traffic is not None:
+        e["traffic_bytes"] = traffic
+    if extra:
+        e.update(extra)
+    log(f"  {name:34s} {e['us_mean']:9.2f} us  {e['GBps']:8.1f} GB/s  "
+        f"{100 * e['frac_of_peak']:5.1f}% of 8 TB/s")
+    return e
+
+
+def sets_for(bytes_per_set: int, floor: int = 1 << 30, most: int = 64) -> int:
+    return max(2, min(most, -(-floor // max(1, bytes_per_set)) + 1))
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the kernels are single-GPU; this build has no "
+              f"multi-GPU path): --gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+    import numpy as np  # noqa: F401
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from __graft_entry__ import load_llmk
+    llmk = load_llmk()
+    import llmk.workloads as wl
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    timer = Timer(torch)
+    traffic = read_traffic()
+    K, W = args.steps, args.warmup
+    log(f"device: {torch.cuda.get_device_name(dev)}  steps={K} warmup={W}")
+    kernels = {}
+
+    # ---------------- headline: fused residual add + RMSNorm [8192, 2048] ----------------
+    rows, hidden = 8192, wl.HIDDEN
+    nbytes = wl.bytes_add_rmsnorm(rows, hidden)
+    R = sets_for(3 * rows * hidden * 2)
+    sets = [wl.add_rmsnorm_inputs(rows, hidden, seed=wl.SEED_BASE + 2 + 100 * i) for i in range(R)]
+    w = sets[0]["w"]
+
+    def launch_add_rmsnorm(i):
+        s = sets[i]
+        llmk.add_rmsnorm(s["residual"], s["x"], w, s["out"], rows, hidden, wl.EPS)
+
+    t = timer.run(launch_add_rmsnorm, R, K, W)
+    head = kernel_entry("add_rmsnorm [8192,2048]", nbytes, t, traffic.get("add_rmsnorm"),
+                        {"sets": R})
+    kernels["add_rmsnorm_8192x2048"] = head
+    headline_wall = t["wall_s"]
+    cpu_inputs = {k: sets[0][k].cpu().contiguous() for k in ("residual", "x", "w")}
+    del sets
+    torch.cuda.empty_cache()
+
+    if args.kernels == "all":
+        # config 1: RMSNorm [16, 2048] (the reference's CPU-plumbing case, on the GPU)
+        sets1 = [wl.add_rmsnorm_inputs(16, hidden, seed=wl.SEED_BASE + 1 + 100 * i)
+                 for i in range(8)]
+        t = timer.run(lambda i: llmk.rmsnorm(sets1[i]["x"], sets1[i]["w"], sets1[i]["out"], 16,
+                                             hidden, wl.EPS), 8, K, W)
+        kernels["rmsnorm_16x2048"] = kernel_entry("rmsnorm [16,2048]",
+                                                  wl.bytes_rmsnorm(16, hidden), t,
+                                                  traffic.get("rmsnorm_16"))
+        del sets1
+
+        # config 3: RoPE, Q [8192,32,64] + K [8192,8,64], positions < 131072
+        inv = torch.tensor(llmk.compute_rope_inv_freq(wl.HEAD_DIM, *wl.ROPE_ARGS),
+                           dtype=torch.float32, device=dev)
+        T = 8192
+        R3 = sets_for(wl.bytes_rope(T, wl.N_HEADS, wl.N_KV, wl.HEAD_DIM) // 2)
+        sets3 = [wl.rope_inputs(T, seed=wl.SEED_BASE + 3 + 100 * i, inv_freq=inv)
+                 for i in range(R3)]
+        t = timer.run(lambda i: llmk.rope_apply(sets3[i]["q"], sets3[i]["k"],
+                                                sets3[i]["positions"], inv, T, wl.N_HEADS,
+                                                wl.N_KV, wl.HEAD_DIM), R3, K, W)
+        kernels["rope_8192"] = kernel_entry(
+            "rope_apply Q+K [8192 tokens]", wl.bytes_rope(T, wl.N_HEADS, wl.N_KV, wl.HEAD_DIM),
+            t, traffic.get("rope"), {"sets": R3})
+        del sets3
+
+        # config 4a: SwiGLU [8192, 8192]
+        n = 8192 * wl.INTER
+        R4 = sets_for(wl.bytes_swiglu(n))
+        sets4 = [wl.swiglu_inputs(seed=wl.SEED_BASE + 4 + 100 * i) for i in range(R4)]
+        t = timer.run(lambda i: llmk.swiglu(sets4[i]["gate"], sets4[i]["up"], sets4[i]["out"], n),
+                      R4, K, W)
+        kernels["swiglu_8192x8192"] = kernel_entry("swiglu [8192,8192]", wl.bytes_swiglu(n), t,
+                                                   traffic.get("swiglu"), {"sets": R4})
+        del sets4
+        torch.cuda.empty_cache()
+
+        # config 4b: embedding gather of 8192 ids from [128256, 2048]. Four tables (2.1 GB)
+        # so a row read by one launch is rarely still cached when its table comes round again.
+        tables = [wl.embedding_table(seed=wl.SEED_BASE + 40 + 100 * i) for i in range(4)]
+        R5 = 16
+        sets5 = [wl.embedding_inputs(8192, tables[i % 4], seed=wl.SEED_BASE + 41 + 100 * i)
+                 for i in range(R5)]
+        t = timer.run(lambda i: llmk.embedding_lookup(sets5[i]["table"], sets5[i]["ids"],
+                                                      sets5[i]["out"], 8192, hidden,
+                                                      check_indices=False), R5, K, W)
+        kernels["embedding_8192"] = kernel_entry(
+            "embedding_lookup 8192 of 128256", wl.bytes_embedding(8192, hidden), t,
+            traffic.get("embedding"), {"sets": R5, "tables": 4,
+                                       "note": "ids uniform; ~3% duplicate rows per launch"})
+        table = tables[0]
+        del sets5, tables
+
+        # config 5: decode-step non-GEMM pass, 16 layers x 256 sequences, in a HIP graph
+        p = wl.decode_pass_inputs(inv, table=table)
+        dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables,
+                                    p.positions, p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
+                                    n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
+                                    page_size=wl.PAGE, max_pages=p.max_pages, eps=wl.EPS)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            dp.run()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            dp.run()
+        t = timer.run(lambda i: graph.replay(), 1, max(20, K // 4), max(5, W // 4))
+        kernels["decode_pass_16x256"] = kernel_entry(
+            "decode pass 16 layers x 256 (graph)", wl.bytes_decode_pass(256, 16), t, None,
+            {"launches": 1 + 3 * 16, "layers": 16, "seqs": 256,
+             "note": "footprint 321 MB (> 256 MB MALL); one HIP graph of 49 kernels"})
+        t = timer.run(lambda i: dp.run(), 1, max(20, K // 4), max(5, W // 4))
+        kernels["decode_pass_16x256_eager"] = kernel_entry(
+            "decode pass 16 layers x 256 (eager)", wl.bytes_decode_pass(256, 16), t)
+        del p, dp, graph, table
+        torch.cuda.empty_cache()
+
+        # copy probe: practical HBM ceiling (ref: bench/bandwidth.cu)
+        nb = 1 << 30
+        bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(4)]
+        t = timer.run(lambda i: llmk.copy_bytes(bufs[2 * (i % 2)], bufs[2 * (i % 2) + 1], nb),
+                      2, max(20, K // 4), 5)
+        kernels["copy_1GiB"] = kernel_entry("copy probe 1 GiB", 2 * nb, t,
+                                            traffic.get("copy"))
+        del bufs
+
+    # ---------------- CPU baseline: the scalar oracle on the host cores ----------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cpu_inputs, rows, hidden, nbytes, args.cpu_seconds, wl.EPS)
+
+    value = nbytes * K / headline_wall / 1e9
+    rec = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": round(headline_wall / K * 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "fused residual add + RMSNorm fp16 [8192,2048] (configs[1])",
+                   "rows": rows, "hidden": hidden, "eps": wl.EPS, "accumulate": "f32",
+                   "input_sets": head["sets"], "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(head["GBps"] / PEAK_GBS, 4),
+                     "traffic": traffic.get("add_rmsnorm")},
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+def cpu_baseline(inp, rows, hidden, nbytes, seconds, eps):
+    """Times the oracle's add_rmsnorm on host copies of the first input set: all usable cores
+    (threads split by rows), then one core, over a bounded number of full [8192, 2048] passes."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    oracle.lib()
+    r0 = inp["residual"].numpy().view(np.uint16).copy()
+    x = inp["x"].numpy().view(np.uint16)
+    w = inp["w"].numpy().view(np.uint16)
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+
+    def timed(nthreads, budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            r = r0.copy()
+            oracle.add_rmsnorm(r, x, w, rows, hidden, eps, threads=nthreads)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return reps, el
+
+    reps, el = timed(threads, seconds * 0.7)
+    reps1, el1 = timed(1, seconds * 0.3)
+    v = nbytes * reps / el / 1e9
+    v1 = nbytes * reps1 / el1 / 1e9
+    log(f"  CPU oracle add_rmsnorm: {v:.2f} GB/s on {threads} threads, {v1:.2f} GB/s on 1")
+    return {"value": round(v, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} full [8192,2048] add_rmsnorm passes ({el:.1f} s) of the scalar C "
+                      f"oracle, rows split over {threads} threads",
+            "one_core": {"value": round(v1, 3), "unit": "GB/s", "cores": 1,
+                         "sample": f"{reps1} passes ({el1:.1f} s)"}}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

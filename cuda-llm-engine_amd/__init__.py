@@ -1,0 +1,360 @@
+"""llmk -- Python face of libllmk, the MI355X (gfx950) non-GEMM layer kernels.
+
+The functions below carry the names and argument lists of the reference engine's C++ launchers
+(JayeshNikam36/cuda-llm-engine, kernels/*.cuh) and call libllmk's C-ABI (include/llmk.h)
+through ctypes. Tensors are torch CUDA tensors (torch provides device memory and streams only;
+all compute is libllmk's HIP kernels). ``stream=None`` means torch's current stream.
+
+Errors: a violated precondition raises ``LlmkError`` before anything is launched. Besides the
+C-ABI's own checks, every function verifies here that each tensor holds at least the elements
+the kernel will touch, and (``check_indices=True``, the default, at the cost of a device sync)
+that token ids, page numbers and positions address only rows that exist, so that a kernel is
+never launched on operands that do not fit it.
+
+There is no CPU fallback: if libllmk.so is missing, importing this package raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libllmk.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "llmk.h")
+
+LLMK_OK = 0
+LLMK_ERR_INVALID_VALUE = 10001
+LLMK_ERR_SHAPE = 10002
+LLMK_ERR_ALIGNMENT = 10003
+LLMK_ERR_UNSUPPORTED = 10004
+
+
+class LlmkError(RuntimeError):
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn}: {msg} (status {status})")
+        self.status = status
+
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"libllmk.so not found at {LIB_PATH}: build it first (python -c "
+        "'import __graft_entry__; __graft_entry__.build()')")
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+_f = ctypes.c_float
+_d = ctypes.c_double
+
+
+class DecodePass(ctypes.Structure):
+    """Mirror of ``struct llmk_decode_pass`` (include/llmk.h)."""
+    _fields_ = [
+        ("n_seqs", _i), ("n_layers", _i), ("hidden", _i), ("n_heads", _i),
+        ("n_kv_heads", _i), ("head_dim", _i), ("inter", _i), ("page_size", _i),
+        ("max_pages", _i), ("eps", _f),
+        ("embed_table", _vp), ("token_ids", _vp), ("residual", _vp),
+        ("block_tables", _vp), ("positions", _vp), ("inv_freq", _vp),
+        ("x", ctypes.POINTER(_vp)), ("norm_w", ctypes.POINTER(_vp)),
+        ("normed", ctypes.POINTER(_vp)), ("q", ctypes.POINTER(_vp)),
+        ("k", ctypes.POINTER(_vp)), ("v", ctypes.POINTER(_vp)),
+        ("k_pool", ctypes.POINTER(_vp)), ("v_pool", ctypes.POINTER(_vp)),
+        ("gate", ctypes.POINTER(_vp)), ("up", ctypes.POINTER(_vp)),
+        ("act", ctypes.POINTER(_vp)),
+    ]
+
+
+_SIGS = {
+    "llmk_error_string": (ctypes.c_char_p, [_i]),
+    "llmk_version": (_i, []),
+    "llmk_embedding_lookup": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "llmk_residual_add": (_i, [_vp, _vp, _vp, _sz, _vp]),
+    "llmk_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "llmk_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
+    "llmk_compute_rope_inv_freq": (_i, [_i, _d, _d, _d, _d, _d, ctypes.POINTER(_f)]),
+    "llmk_rope_apply": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "llmk_swiglu": (_i, [_vp, _vp, _vp, _sz, _vp]),
+    "llmk_kv_scatter": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "llmk_kv_scatter_batch": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "llmk_rope_kv_scatter_batch": (_i, [_vp] * 8 + [_i] * 6 + [_vp]),
+    "llmk_copy_bytes": (_i, [_vp, _vp, _sz, _vp]),
+    "llmk_decode_nongemm_pass": (_i, [ctypes.POINTER(DecodePass), _vp]),
+}
+
+_lib = ctypes.CDLL(LIB_PATH)
+for _name, (_res, _args) in _SIGS.items():
+    _fn = getattr(_lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def lib() -> ctypes.CDLL:
+    return _lib
+
+
+def exported_symbols_declared_in_header() -> list[str]:
+    """Names of every function declared in include/llmk.h."""
+    with open(HEADER_PATH) as f:
+        text = f.read()
+    return re.findall(r"LLMK_API\s+[\w\s\*]*?\b(llmk_\w+)\s*\(", text)
+
+
+def error_string(status: int) -> str:
+    return _lib.llmk_error_string(status).decode()
+
+
+def version() -> int:
+    return _lib.llmk_version()
+
+
+def _check(fn: str, status: int) -> None:
+    if status != LLMK_OK:
+        raise LlmkError(fn, status, error_string(status))
+
+
+def _fail(fn: str, msg: str):
+    raise LlmkError(fn, LLMK_ERR_INVALID_VALUE, msg)
+
+
+def _dev(fn: str, t: torch.Tensor, dtype: torch.dtype, min_numel: int, name: str) -> int:
+    if not isinstance(t, torch.Tensor):
+        _fail(fn, f"{name} must be a torch tensor")
+    if t.device.type != "cuda":
+        _fail(fn, f"{name} must be a CUDA tensor, got {t.device}")
+    if t.dtype != dtype:
+        _fail(fn, f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        _fail(fn, f"{name} must be contiguous")
+    if t.numel() < min_numel:
+        _fail(fn, f"{name} holds {t.numel()} elements, the call touches {min_numel}")
+    return t.data_ptr()
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return int(stream)
+
+
+def _range_check(fn: str, t: torch.Tensor, n: int, lo: int, hi: int, name: str) -> None:
+    if n == 0:
+        return
+    v = t.reshape(-1)[:n]
+    mn, mx = int(v.min()), int(v.max())
+    if mn < lo or mx >= hi:
+        _fail(fn, f"{name} values must lie in [{lo}, {hi}), got [{mn}, {mx}]")
+
+
+# ---------------------------------------------------------------------------------------------
+# operators (ref: kernels/*.cuh)
+# ---------------------------------------------------------------------------------------------
+def embedding_lookup(table, ids, out, n_tokens: int, hidden: int, stream=None,
+                     check_indices: bool = True) -> None:
+    """out[t] = table[ids[t]] (ref: kernels/embedding.cuh:6-7)."""
+    fn = "embedding_lookup"
+    if table.dim() != 2 or table.shape[1] != hidden:
+        _fail(fn, f"table must be [vocab, {hidden}]")
+    pt = _dev(fn, table, torch.float16, 0, "table")
+    pi = _dev(fn, ids, torch.int32, n_tokens, "ids")
+    po = _dev(fn, out, torch.float16, n_tokens * hidden, "out")
+    if check_indices:
+        _range_check(fn, ids, n_tokens, 0, table.shape[0], "ids")
+    _check(fn, _lib.llmk_embedding_lookup(pt, pi, po, n_tokens, hidden, _stream(stream)))
+
+
+def residual_add(a, b, out, n: int, stream=None) -> None:
+    """out = a + b in fp16, out may be a (ref: kernels/residual_add.cuh:6)."""
+    fn = "residual_add"
+    pa = _dev(fn, a, torch.float16, n, "a")
+    pb = _dev(fn, b, torch.float16, n, "b")
+    po = _dev(fn, out, torch.float16, n, "out")
+    _check(fn, _lib.llmk_residual_add(pa, pb, po, n, _stream(stream)))
+
+
+def rmsnorm(x, w, out, n_rows: int, hidden: int, eps: float, stream=None) -> None:
+    """RMSNorm of n_rows rows (ref: kernels/rmsnorm.cuh:6-7)."""
+    fn = "rmsnorm"
+    px = _dev(fn, x, torch.float16, n_rows * hidden, "x")
+    pw = _dev(fn, w, torch.float16, hidden, "w")
+    po = _dev(fn, out, torch.float16, n_rows * hidden, "out")
+    _check(fn, _lib.llmk_rmsnorm(px, pw, po, n_rows, hidden, eps, _stream(stream)))
+
+
+def add_rmsnorm(residual, x, w, out, n_rows: int, hidden: int, eps: float, stream=None) -> None:
+    """residual += x (fp16, in place), out = rmsnorm(residual)."""
+    fn = "add_rmsnorm"
+    pr = _dev(fn, residual, torch.float16, n_rows * hidden, "residual")
+    px = _dev(fn, x, torch.float16, n_rows * hidden, "x")
+    pw = _dev(fn, w, torch.float16, hidden, "w")
+    po = _dev(fn, out, torch.float16, n_rows * hidden, "out")
+    _check(fn, _lib.llmk_add_rmsnorm(pr, px, pw, po, n_rows, hidden, eps, _stream(stream)))
+
+
+def compute_rope_inv_freq(head_dim: int, theta: float, factor: float, low_freq_factor: float,
+                          high_freq_factor: float, original_max_pos: float) -> list[float]:
+    """Host function: head_dim/2 llama3-scaled rotation speeds (ref: kernels/rope.cuh:7-9)."""
+    if head_dim <= 0 or head_dim % 2:
+        _fail("compute_rope_inv_freq", "head_dim must be even and positive")
+    buf = (ctypes.c_float * (head_dim // 2))()
+    _check("compute_rope_inv_freq",
+           _lib.llmk_compute_rope_inv_freq(head_dim, theta, factor, low_freq_factor,
+                                           high_freq_factor, original_max_pos, buf))
+    return list(buf)
+
+
+def rope_apply(q, k, positions, inv_freq, n_tokens: int, n_heads: int, n_kv_heads: int,
+               head_dim: int, stream=None) -> None:
+    """In-place RoPE of q and k (ref: kernels/rope.cuh:13-15)."""
+    fn = "rope_apply"
+    pq = _dev(fn, q, torch.float16, n_tokens * n_heads * head_dim, "q") if n_heads else 0
+    pk = _dev(fn, k, torch.float16, n_tokens * n_kv_heads * head_dim, "k") if n_kv_heads else 0
+    pp = _dev(fn, positions, torch.int32, n_tokens, "positions")
+    pf = _dev(fn, inv_freq, torch.float32, head_dim // 2, "inv_freq")
+    _check(fn, _lib.llmk_rope_apply(pq, pk, pp, pf, n_tokens, n_heads, n_kv_heads, head_dim,
+                                    _stream(stream)))
+
+
+def swiglu(gate, up, out, n: int, stream=None) -> None:
+    """out = silu(gate) * up (ref: kernels/swiglu.cuh:6)."""
+    fn = "swiglu"
+    pg = _dev(fn, gate, torch.float16, n, "gate")
+    pu = _dev(fn, up, torch.float16, n, "up")
+    po = _dev(fn, out, torch.float16, n, "out")
+    _check(fn, _lib.llmk_swiglu(pg, pu, po, n, _stream(stream)))
+
+
+def _pool_rows(fn: str, pool, kvdim: int) -> int:
+    if pool.numel() % kvdim:
+        _fail(fn, f"pool size {pool.numel()} is not a whole number of {kvdim}-wide rows")
+    return pool.numel() // kvdim
+
+
+def kv_scatter(src, pool, block_table, start_pos: int, T: int, page_size: int, kvdim: int,
+               stream=None, check_indices: bool = True) -> None:
+    """Prefill scatter of T rows into pages (ref: kernels/kv_scatter.cuh:7-8)."""
+    fn = "kv_scatter"
+    if T > 0 and (start_pos < 0 or page_size <= 0):
+        _fail(fn, "start_pos must be >= 0 and page_size > 0")
+    n_table = (start_pos + T - 1) // page_size + 1 if T > 0 else 0
+    ps = _dev(fn, src, torch.float16, T * kvdim, "src")
+    pp = _dev(fn, pool, torch.float16, 0, "pool")
+    pt = _dev(fn, block_table, torch.int32, n_table, "block_table")
+    if check_indices and T > 0:
+        rows = _pool_rows(fn, pool, kvdim)
+        first = start_pos // page_size
+        _range_check(fn, block_table[first:n_table], n_table - first, 0, rows // page_size,
+                     "block_table")
+    _check(fn, _lib.llmk_kv_scatter(ps, pp, pt, start_pos, T, page_size, kvdim, _stream(stream)))
+
+
+def _check_batch_tables(fn, block_tables, positions, pools, n, max_pages, page_size, kvdim):
+    _range_check(fn, positions, n, 0, max_pages * page_size, "positions")
+    rows = min(_pool_rows(fn, p, kvdim) for p in pools)
+    pos = positions[:n].long()
+    pages = block_tables.reshape(-1)[:n * max_pages].view(n, max_pages)
+    used = pages.gather(1, (pos // page_size).unsqueeze(1)).squeeze(1)
+    _range_check(fn, used, n, 0, rows // page_size, "block_tables (addressed entries)")
+
+
+def kv_scatter_batch(src, pool, block_tables, positions, n: int, max_pages: int,
+                     page_size: int, kvdim: int, stream=None, check_indices: bool = True) -> None:
+    """Decode scatter, one row per sequence (ref: kernels/kv_scatter.cuh:12-13)."""
+    fn = "kv_scatter_batch"
+    ps = _dev(fn, src, torch.float16, n * kvdim, "src")
+    pp = _dev(fn, pool, torch.float16, 0, "pool")
+    pt = _dev(fn, block_tables, torch.int32, n * max_pages, "block_tables")
+    pq = _dev(fn, positions, torch.int32, n, "positions")
+    if check_indices and n > 0:
+        _check_batch_tables(fn, block_tables, positions, [pool], n, max_pages, page_size, kvdim)
+    _check(fn, _lib.llmk_kv_scatter_batch(ps, pp, pt, pq, n, max_pages, page_size, kvdim,
+                                          _stream(stream)))
+
+
+def rope_kv_scatter_batch(q, k, v, k_pool, v_pool, block_tables, positions, inv_freq, n: int,
+                          max_pages: int, page_size: int, n_heads: int, n_kv_heads: int,
+                          head_dim: int, stream=None, check_indices: bool = True) -> None:
+    """Fused decode RoPE of q (in place) and k, with k and v scattered into their pools."""
+    fn = "rope_kv_scatter_batch"
+    kvdim = n_kv_heads * head_dim
+    pq = _dev(fn, q, torch.float16, n * n_heads * head_dim, "q") if n_heads else 0
+    pk = _dev(fn, k, torch.float16, n * kvdim, "k")
+    pv = _dev(fn, v, torch.float16, n * kvdim, "v")
+    pkp = _dev(fn, k_pool, torch.float16, 0, "k_pool")
+    pvp = _dev(fn, v_pool, torch.float16, 0, "v_pool")
+    pt = _dev(fn, block_tables, torch.int32, n * max_pages, "block_tables")
+    pp = _dev(fn, positions, torch.int32, n, "positions")
+    pf = _dev(fn, inv_freq, torch.float32, head_dim // 2, "inv_freq")
+    if check_indices and n > 0:
+        _check_batch_tables(fn, block_tables, positions, [k_pool, v_pool], n, max_pages,
+                            page_size, kvdim)
+    _check(fn, _lib.llmk_rope_kv_scatter_batch(pq, pk, pv, pkp, pvp, pt, pp, pf, n, max_pages,
+                                               page_size, n_heads, n_kv_heads, head_dim,
+                                               _stream(stream)))
+
+
+def copy_bytes(src, dst, nbytes: int, stream=None) -> None:
+    """16-byte vector device copy (bandwidth probe)."""
+    fn = "copy_bytes"
+    if src.numel() * src.element_size() < nbytes or dst.numel() * dst.element_size() < nbytes:
+        _fail(fn, "buffers smaller than nbytes")
+    if src.device.type != "cuda" or dst.device.type != "cuda":
+        _fail(fn, "buffers must be CUDA tensors")
+    _check(fn, _lib.llmk_copy_bytes(src.data_ptr(), dst.data_ptr(), nbytes, _stream(stream)))
+
+
+class DecodeNonGemmPass:
+    """The non-GEMM decode pass over caller-owned tensors: embedding into ``residual``, then per
+    layer add+RMSNorm, fused RoPE + K/V scatter, and SwiGLU (``llmk_decode_nongemm_pass``).
+
+    ``layers`` is a list of dicts with the per-layer tensors x, norm_w, normed, q, k, v,
+    k_pool, v_pool, gate, up, act. The descriptor (host pointer arrays) is built once; ``run``
+    enqueues the whole pass on one stream and can be captured into a CUDA/HIP graph.
+    """
+
+    def __init__(self, embed_table, token_ids, residual, block_tables, positions, inv_freq,
+                 layers, *, n_heads: int, n_kv_heads: int, head_dim: int, inter: int,
+                 page_size: int, max_pages: int, eps: float, check_indices: bool = True):
+        fn = "decode_nongemm_pass"
+        n = token_ids.numel()
+        hidden = residual.shape[-1]
+        kvdim = n_kv_heads * head_dim
+        self._keep = [embed_table, token_ids, residual, block_tables, positions, inv_freq,
+                      layers]
+        d = DecodePass()
+        d.n_seqs, d.n_layers, d.hidden = n, len(layers), hidden
+        d.n_heads, d.n_kv_heads, d.head_dim, d.inter = n_heads, n_kv_heads, head_dim, inter
+        d.page_size, d.max_pages, d.eps = page_size, max_pages, eps
+        if embed_table.dim() != 2 or embed_table.shape[1] != hidden:
+            _fail(fn, f"embed_table must be [vocab, {hidden}]")
+        d.embed_table = _dev(fn, embed_table, torch.float16, 0, "embed_table")
+        d.token_ids = _dev(fn, token_ids, torch.int32, n, "token_ids")
+        d.residual = _dev(fn, residual, torch.float16, n * hidden, "residual")
+        d.block_tables = _dev(fn, block_tables, torch.int32, n * max_pages, "block_tables")
+        d.positions = _dev(fn, positions, torch.int32, n, "positions")
+        d.inv_freq = _dev(fn, inv_freq, torch.float32, head_dim // 2, "inv_freq")
+        need = {"x": n * hidden, "norm_w": hidden, "normed": n * hidden,
+                "q": n * n_heads * head_dim, "k": n * kvdim, "v": n * kvdim, "k_pool": 0,
+                "v_pool": 0, "gate": n * inter, "up": n * inter, "act": n * inter}
+        self._arrays = {}
+        for key, cnt in need.items():
+            arr = (_vp * max(1, len(layers)))()
+            for l, layer in enumerate(layers):
+                arr[l] = _dev(fn, layer[key], torch.float16, cnt, f"layers[{l}].{key}")
+            self._arrays[key] = arr
+            setattr(d, key, ctypes.cast(arr, ctypes.POINTER(_vp)))
+        if check_indices and n > 0:
+            _range_check(fn, token_ids, n, 0, embed_table.shape[0], "token_ids")
+            pools = [layer[p] for layer in layers for p in ("k_pool", "v_pool")]
+            if pools:
+                _check_batch_tables(fn, block_tables, positions, pools, n, max_pages,
+                                    page_size, kvdim)
+        self._desc = d
+
+    def run(self, stream=None) -> None:
+        _check("decode_nongemm_pass",
+               _lib.llmk_decode_nongemm_pass(ctypes.byref(self._desc), _stream(stream)))

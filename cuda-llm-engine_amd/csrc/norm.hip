@@ -1,0 +1,212 @@
+// Residual add, RMSNorm and the fused residual add + RMSNorm for gfx950.
+//
+// Semantics follow the reference launchers (ref: kernels/residual_add.cu:5-18,
+// kernels/rmsnorm.cu:9-68); the fused kernel equals residual_add followed by rmsnorm on the
+// updated residual (ref: engine/batched.cu:64->66).
+//
+// Layout and mapping: rows of `hidden` fp16 values, row-major and contiguous. One wave64 owns
+// one row: lane l holds the 16-byte vectors l, l+64, l+128, ... of the row in registers (for
+// hidden = 2048 that is 4 vectors per tensor per lane, each load instruction covering 1 KiB of
+// consecutive memory). The row is read from HBM exactly once; the sum of squares is reduced
+// across the wave with DPP permutes, so no LDS and no barrier is involved. Rows wider than
+// 64 * 8 * 16 = 8192 values take a block-per-row kernel that reads the row twice (the second
+// time from L2).
+#include "common.hpp"
+
+namespace llmk {
+
+// ----------------------------------------------------------------------------------------------
+// residual_add: out = fp16(a + b). Packed fp16 add == fp32 add then RNE rounding (see common.hpp).
+// ----------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_residual_add_vec(const f16* a, const f16* b, f16* out, size_t nvec, size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (size_t i = tid; i < nvec; i += stride) {
+    const f16x8 va = as_h8(ld16(a + 8 * i));
+    const f16x8 vb = as_h8(ld16(b + 8 * i));
+    st16(out + 8 * i, as_u4(va + vb));
+  }
+  const size_t t = nvec * 8 + tid;  // the n % 8 trailing values
+  if (t < n) out[t] = a[t] + b[t];
+}
+
+// Any-alignment path: one fp16 value per thread per step.
+__global__ void __launch_bounds__(256)
+k_residual_add_scalar(const f16* a, const f16* b, f16* out, size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = a[i] + b[i];
+}
+
+// ----------------------------------------------------------------------------------------------
+// RMSNorm, one wave per row. VPL = 16-byte vectors per lane per tensor.
+// FUSED: resid <- fp16(resid + x) first, and the norm is taken of the updated resid.
+// FULL: vpr == 64 * VPL, every lane owns exactly VPL vectors (no bounds tests).
+// ----------------------------------------------------------------------------------------------
+template <int VPL, bool FUSED, bool FULL>
+__global__ void __launch_bounds__(256)
+k_rmsnorm_wave(const f16* x, f16* resid, const f16* __restrict__ w, f16* out, int n_rows,
+               int vpr, float hidden_f, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= n_rows) return;  // uniform per wave
+  const size_t base = (size_t)row * vpr * 8;
+  auto owned = [&](int v) { return FULL || v < vpr; };
+
+  f16x8 h[VPL], wv[VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int v = lane + 64 * k;
+    if (owned(v)) {
+      h[k] = as_h8(ld16(x + base + 8 * v));
+      if (FUSED) h[k] = as_h8(ld16(resid + base + 8 * v)) + h[k];
+      wv[k] = as_h8(ld16(w + 8 * v));
+    } else {
+      h[k] = (f16x8)(f16)0;
+      wv[k] = (f16x8)(f16)0;
+    }
+  }
+  if (FUSED) {
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int v = lane + 64 * k;
+      if (owned(v)) st16(resid + base + 8 * v, as_u4(h[k]));
+    }
+  }
+
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = (float)h[k][j];
+      ss = ss + f * f;
+    }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / __builtin_sqrtf(ss / hidden_f + eps);
+
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int v = lane + 64 * k;
+    if (owned(v)) {
+      f16x8 a;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = (f16)((float)h[k][j] * inv);
+      st16_stream(out + base + 8 * v, as_u4(wv[k] * a));
+    }
+  }
+}
+
+// Wide rows: one 256-thread block per row, two passes over the row.
+template <bool FUSED>
+__global__ void __launch_bounds__(256)
+k_rmsnorm_block(const f16* x, f16* resid, const f16* __restrict__ w, f16* out, int vpr,
+                float hidden_f, float eps) {
+  __shared__ float part[4];
+  const size_t base = (size_t)blockIdx.x * vpr * 8;
+  float ss = 0.f;
+  for (int v = threadIdx.x; v < vpr; v += 256) {
+    f16x8 h = as_h8(ld16(x + base + 8 * v));
+    if (FUSED) {
+      h = as_h8(ld16(resid + base + 8 * v)) + h;
+      st16(resid + base + 8 * v, as_u4(h));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = (float)h[j];
+      ss = ss + f * f;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float inv = 1.0f / __builtin_sqrtf(total / hidden_f + eps);
+  // Each thread re-reads exactly the vectors it wrote above, so its own stores are visible.
+  const f16* src = FUSED ? resid : x;
+  for (int v = threadIdx.x; v < vpr; v += 256) {
+    const f16x8 h = as_h8(ld16(src + base + 8 * v));
+    const f16x8 wv = as_h8(ld16(w + 8 * v));
+    f16x8 a;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = (f16)((float)h[j] * inv);
+    st16(out + base + 8 * v, as_u4(wv * a));
+  }
+}
+
+template <bool FUSED>
+static int rmsnorm_launch(const f16* x, f16* resid, const f16* w, f16* out, int n_rows,
+                          int hidden, float eps, hipStream_t stream) {
+  const int vpr = hidden / 8;
+  const float hf = (float)hidden;
+  const int vpl = (vpr + 63) / 64;
+  // Few rows: one wave per block so the rows spread over as many CUs as possible.
+  const int wpb = n_rows >= 4096 ? 4 : 1;
+  const dim3 grid(ceil_div((size_t)n_rows, (size_t)wpb)), block(64 * wpb);
+#define LLMK_NORM_CASE(V)                                                                     \
+  return vpr == 64 * V ? launch(k_rmsnorm_wave<V, FUSED, true>, grid, block, 0, stream, x, resid, \
+                                w, out, n_rows, vpr, hf, eps)                                    \
+                       : launch(k_rmsnorm_wave<V, FUSED, false>, grid, block, 0, stream, x,      \
+                                resid, w, out, n_rows, vpr, hf, eps)
+  if (vpl <= 1) LLMK_NORM_CASE(1);
+  if (vpl <= 2) LLMK_NORM_CASE(2);
+  if (vpl <= 4) LLMK_NORM_CASE(4);
+  if (vpl <= 8) LLMK_NORM_CASE(8);
+  if (vpl <= 16) LLMK_NORM_CASE(16);
+#undef LLMK_NORM_CASE
+  return launch(k_rmsnorm_block<FUSED>, dim3(n_rows), dim3(256), 0, stream, x, resid, w, out,
+                vpr, hf, eps);
+}
+
+}  // namespace llmk
+
+using namespace llmk;
+
+extern "C" int llmk_residual_add(const uint16_t* a, const uint16_t* b, uint16_t* out, size_t n,
+                                 void* stream) {
+  if (n == 0) return LLMK_OK;
+  if (!a || !b || !out) return LLMK_ERR_INVALID_VALUE;
+  const f16* pa = reinterpret_cast<const f16*>(a);
+  const f16* pb = reinterpret_cast<const f16*>(b);
+  f16* po = reinterpret_cast<f16*>(out);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (aligned16(a) && aligned16(b) && aligned16(out)) {
+    const size_t nvec = n / 8;
+    const size_t need = nvec > 0 ? nvec : 1;
+    const unsigned blocks = ceil_div(need, 256) < 8192u ? ceil_div(need, 256) : 8192u;
+    return launch(k_residual_add_vec, dim3(blocks), dim3(256), 0, s, pa, pb, po, nvec, n);
+  }
+  const unsigned blocks = ceil_div(n, 256) < 8192u ? ceil_div(n, 256) : 8192u;
+  return launch(k_residual_add_scalar, dim3(blocks), dim3(256), 0, s, pa, pb, po, n);
+}
+
+static int check_norm_args(const void* x, const void* w, const void* out, int n_rows,
+                           int hidden) {
+  if (n_rows < 0 || hidden <= 0) return LLMK_ERR_INVALID_VALUE;
+  if (n_rows == 0) return LLMK_OK;
+  if (!x || !w || !out) return LLMK_ERR_INVALID_VALUE;
+  if (hidden % 8 != 0) return LLMK_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out)) return LLMK_ERR_ALIGNMENT;
+  return -1;  // arguments fine, proceed
+}
+
+extern "C" int llmk_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int n_rows,
+                            int hidden, float eps, void* stream) {
+  const int st = check_norm_args(x, w, out, n_rows, hidden);
+  if (st != -1) return st;
+  return rmsnorm_launch<false>(reinterpret_cast<const f16*>(x), nullptr,
+                               reinterpret_cast<const f16*>(w), reinterpret_cast<f16*>(out),
+                               n_rows, hidden, eps, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int llmk_add_rmsnorm(uint16_t* residual, const uint16_t* x, const uint16_t* w,
+                                uint16_t* out, int n_rows, int hidden, float eps, void* stream) {
+  int st = check_norm_args(x, w, out, n_rows, hidden);
+  if (st != -1) return st;
+  if (!residual) return LLMK_ERR_INVALID_VALUE;
+  if (!aligned16(residual)) return LLMK_ERR_ALIGNMENT;
+  return rmsnorm_launch<true>(reinterpret_cast<const f16*>(x), reinterpret_cast<f16*>(residual),
+                              reinterpret_cast<const f16*>(w), reinterpret_cast<f16*>(out),
+                              n_rows, hidden, eps, static_cast<hipStream_t>(stream));
+}

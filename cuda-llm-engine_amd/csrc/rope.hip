@@ -1,0 +1,233 @@
+// Rotary position embedding with the Llama-3 rotation speeds, and its fusion with the paged KV
+// scatter of the decode step.
+//
+// Semantics (ref: kernels/rope.cu:27-44): for token t, pair i < head_dim/2 (element i with
+// element i + head_dim/2), angle a = float(pos[t]) * inv_freq[i] as one fp32 product,
+// c = r16(cos a), s = r16(sin a), x1' = fp16(r16(x1*c) - r16(x2*s)), x2' = fp16(r16(x2*c) +
+// r16(x1*s)). Once c and s are fp16 values, every remaining step is an fp16 multiply or add of
+// two fp16 values rounded to fp16, which the packed fp16 instructions compute bit for bit.
+//
+// Work split: a block owns `tpb` consecutive tokens. Phase 1 computes the tpb * head_dim/2 (cos,
+// sin) pairs once each with the full-range sincosf and keeps them in LDS as fp16 (the reference
+// evaluates sincosf once per head, 40x as often). Phase 2 walks the (token, head, j) tasks: a
+// task loads the 16-byte vector j of the first half of one head row and vector j of the second
+// half, which hold exactly the 8 pairs (8j .. 8j+7, +head_dim/2), rotates them with four packed
+// multiplies and two packed adds per 2 values, and stores both vectors. Q and K rows are read
+// and written once each.
+//
+// Fused decode variant (replaces ref: engine/batched.cu:55-58): the K task writes its rotated
+// vectors to the K pool row of its sequence instead of back to k, and V tasks copy the value
+// row to the V pool at the same address (ref: kernels/kv_scatter.cu:17-23).
+#include <math.h>
+
+#include "common.hpp"
+
+namespace llmk {
+
+// Unsigned division by a launch-constant divisor with a multiply-high (valid for n < 2^31).
+struct FastDiv {
+  uint32_t d, m, s;
+};
+static FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+  return FastDiv{d, (uint32_t)m, s};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
+  return (__umulhi(n, f.m) + n) >> f.s;
+}
+
+// HV = 16-byte vectors per half head row (head_dim = 16 * HV).
+template <int HV, bool FUSED>
+__global__ void __launch_bounds__(256)
+k_rope_vec(f16* q, f16* k, const f16* __restrict__ v, f16* k_pool, f16* v_pool,
+           const int* __restrict__ tables, const int* __restrict__ pos,
+           const float* __restrict__ inv_freq, int n_tokens, int nh, int nkv, int tpb,
+           int max_pages, int page_size, FastDiv per_token_div) {
+  constexpr int HD = 16 * HV, HALF = 8 * HV;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  long long* pool_row = reinterpret_cast<long long*>(smem);       // [tpb] (FUSED only)
+  f16* cs = reinterpret_cast<f16*>(smem + (FUSED ? 8 * tpb : 0));  // [tpb][cos HALF | sin HALF]
+
+  const int t0 = blockIdx.x * tpb;
+  const int ntok = min(tpb, n_tokens - t0);
+
+  for (int e = threadIdx.x; e < ntok * HALF; e += blockDim.x) {
+    const int tt = e / HALF, i = e % HALF;
+    const float a = (float)pos[t0 + tt] * inv_freq[i];
+    float sn, cn;
+    sincosf(a, &sn, &cn);
+    cs[tt * HD + i] = (f16)cn;
+    cs[tt * HD + HALF + i] = (f16)sn;
+  }
+  if (FUSED) {
+    for (int tt = threadIdx.x; tt < ntok; tt += blockDim.x) {
+      const int b = t0 + tt, p = pos[b];
+      const int page = tables[(size_t)b * max_pages + p / page_size];
+      pool_row[tt] = (long long)page * page_size + p % page_size;
+    }
+  }
+  __syncthreads();
+
+  // Tasks per token: nh + nkv rotated heads, plus nkv value rows in the fused variant.
+  const int rows_per_tok = nh + nkv + (FUSED ? nkv : 0);
+  const int tasks = ntok * rows_per_tok * HV;
+  const size_t kvdim = (size_t)nkv * HD;
+  for (int e = threadIdx.x; e < tasks; e += blockDim.x) {
+    const int tt = (int)fdiv((uint32_t)e, per_token_div);
+    const int r = e - tt * rows_per_tok * HV;
+    const int head = r / HV, j = r % HV;
+    const int t = t0 + tt;
+    if (FUSED && head >= nh + nkv) {  // value row: plain copy into the V pool
+      const int hv = head - nh - nkv;
+      const f16* src = v + (size_t)t * kvdim + (size_t)hv * HD + 8 * j;
+      f16* dst = v_pool + pool_row[tt] * kvdim + (size_t)hv * HD + 8 * j;
+      const u32x4 lo = ld16(src), hi = ld16(src + HALF);
+      st16(dst, lo);
+      st16(dst + HALF, hi);
+      continue;
+    }
+    const f16* src;
+    f16* dst;
+    if (head < nh) {
+      src = dst = q + ((size_t)t * nh + head) * HD + 8 * j;
+    } else {
+      const int kh = head - nh;
+      src = k + (size_t)t * kvdim + (size_t)kh * HD + 8 * j;
+      dst = FUSED ? k_pool + pool_row[tt] * kvdim + (size_t)kh * HD + 8 * j
+                  : const_cast<f16*>(src);
+    }
+    const f16x8 x1 = as_h8(ld16(src)), x2 = as_h8(ld16(src + HALF));
+    const f16x8 c = *reinterpret_cast<const f16x8*>(cs + tt * HD + 8 * j);
+    const f16x8 s = *reinterpret_cast<const f16x8*>(cs + tt * HD + HALF + 8 * j);
+    const f16x8 y1 = x1 * c - x2 * s;
+    const f16x8 y2 = x2 * c + x1 * s;
+    st16(dst, as_u4(y1));
+    st16(dst + HALF, as_u4(y2));
+  }
+}
+
+// Any head_dim (even) and any alignment: one pair per thread per step, same arithmetic.
+__global__ void __launch_bounds__(256)
+k_rope_scalar(f16* q, f16* k, const int* __restrict__ pos, const float* __restrict__ inv_freq,
+              int n_tokens, int nh, int nkv, int hd, int tpb) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  f16* cs = reinterpret_cast<f16*>(smem);  // [tpb][cos half | sin half]
+  const int half = hd / 2;
+  const int t0 = blockIdx.x * tpb;
+  const int ntok = min(tpb, n_tokens - t0);
+  for (int e = threadIdx.x; e < ntok * half; e += blockDim.x) {
+    const int tt = e / half, i = e % half;
+    const float a = (float)pos[t0 + tt] * inv_freq[i];
+    float sn, cn;
+    sincosf(a, &sn, &cn);
+    cs[tt * hd + i] = (f16)cn;
+    cs[tt * hd + half + i] = (f16)sn;
+  }
+  __syncthreads();
+  const int per_tok = (nh + nkv) * half;
+  for (int e = threadIdx.x; e < ntok * per_tok; e += blockDim.x) {
+    const int tt = e / per_tok, r = e % per_tok;
+    const int head = r / half, i = r % half;
+    const int t = t0 + tt;
+    f16* row = head < nh ? q + ((size_t)t * nh + head) * hd
+                         : k + ((size_t)t * nkv + (head - nh)) * hd;
+    const f16 c = cs[tt * hd + i], s = cs[tt * hd + half + i];
+    const f16 x1 = row[i], x2 = row[i + half];
+    row[i] = x1 * c - x2 * s;
+    row[i + half] = x2 * c + x1 * s;
+  }
+}
+
+// Tokens per block: enough blocks to cover every CU, but at most 8 tokens (256 angles) per block.
+static int tokens_per_block(int n_tokens) {
+  if (n_tokens >= 8 * 2048) return 8;
+  if (n_tokens >= 4 * 1024) return 4;
+  if (n_tokens >= 2 * 512) return 2;
+  return 1;
+}
+
+template <bool FUSED>
+static int rope_vec_launch(f16* q, f16* k, const f16* v, f16* k_pool, f16* v_pool,
+                           const int* tables, const int* pos, const float* inv_freq,
+                           int n_tokens, int nh, int nkv, int hd, int max_pages, int page_size,
+                           hipStream_t stream) {
+  const int tpb = tokens_per_block(n_tokens);
+  const int hv = hd / 16;
+  const int rows_per_tok = nh + nkv + (FUSED ? nkv : 0);
+  const FastDiv fd = make_fastdiv((uint32_t)(rows_per_tok * hv));
+  const int tasks_per_block = tpb * rows_per_tok * hv;
+  const int threads = tasks_per_block >= 1024 ? 256 : (tasks_per_block >= 256 ? 128 : 64);
+  const dim3 grid(ceil_div((size_t)n_tokens, (size_t)tpb)), block(threads);
+  const size_t lds = (FUSED ? 8 * (size_t)tpb : 0) + (size_t)tpb * hd * sizeof(f16);
+#define LLMK_ROPE_CASE(H)                                                                       \
+  case H:                                                                                       \
+    return launch(k_rope_vec<H, FUSED>, grid, block, lds, stream, q, k, v, k_pool, v_pool,     \
+                  tables, pos, inv_freq, n_tokens, nh, nkv, tpb, max_pages, page_size, fd)
+  switch (hv) {
+    LLMK_ROPE_CASE(1);
+    LLMK_ROPE_CASE(2);
+    LLMK_ROPE_CASE(4);
+    LLMK_ROPE_CASE(8);
+    LLMK_ROPE_CASE(16);
+    default:
+      return LLMK_ERR_UNSUPPORTED;
+  }
+#undef LLMK_ROPE_CASE
+}
+
+}  // namespace llmk
+
+using namespace llmk;
+
+static bool vec_head_dim(int hd) {
+  return hd % 16 == 0 && (hd / 16 == 1 || hd / 16 == 2 || hd / 16 == 4 || hd / 16 == 8 ||
+                          hd / 16 == 16);
+}
+
+extern "C" int llmk_rope_apply(uint16_t* q, uint16_t* k, const int32_t* positions,
+                               const float* inv_freq, int n_tokens, int n_heads, int n_kv_heads,
+                               int head_dim, void* stream) {
+  if (n_tokens < 0 || n_heads < 0 || n_kv_heads < 0 || head_dim <= 0)
+    return LLMK_ERR_INVALID_VALUE;
+  if (n_tokens == 0 || n_heads + n_kv_heads == 0) return LLMK_OK;
+  if (!positions || !inv_freq || (n_heads > 0 && !q) || (n_kv_heads > 0 && !k))
+    return LLMK_ERR_INVALID_VALUE;
+  if (head_dim % 2 != 0) return LLMK_ERR_SHAPE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  f16* pq = reinterpret_cast<f16*>(q);
+  f16* pk = reinterpret_cast<f16*>(k);
+  if (vec_head_dim(head_dim) && aligned16(q) && aligned16(k))
+    return rope_vec_launch<false>(pq, pk, nullptr, nullptr, nullptr, nullptr, positions,
+                                  inv_freq, n_tokens, n_heads, n_kv_heads, head_dim, 0, 1, s);
+  if (head_dim > 4096) return LLMK_ERR_UNSUPPORTED;
+  const int tpb = tokens_per_block(n_tokens);
+  return launch(k_rope_scalar, dim3(ceil_div((size_t)n_tokens, (size_t)tpb)), dim3(256),
+                (size_t)tpb * head_dim * sizeof(f16), s, pq, pk, positions, inv_freq, n_tokens,
+                n_heads, n_kv_heads, head_dim, tpb);
+}
+
+extern "C" int llmk_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                          uint16_t* k_pool, uint16_t* v_pool,
+                                          const int32_t* block_tables, const int32_t* positions,
+                                          const float* inv_freq, int n, int max_pages,
+                                          int page_size, int n_heads, int n_kv_heads,
+                                          int head_dim, void* stream) {
+  if (n < 0 || max_pages <= 0 || page_size <= 0 || n_heads < 0 || n_kv_heads <= 0 ||
+      head_dim <= 0)
+    return LLMK_ERR_INVALID_VALUE;
+  if (n == 0) return LLMK_OK;
+  if ((n_heads > 0 && !q) || !k || !v || !k_pool || !v_pool || !block_tables || !positions ||
+      !inv_freq)
+    return LLMK_ERR_INVALID_VALUE;
+  if (!vec_head_dim(head_dim)) return LLMK_ERR_SHAPE;
+  if ((n_heads > 0 && !aligned16(q)) || !aligned16(k) || !aligned16(v) || !aligned16(k_pool) ||
+      !aligned16(v_pool))
+    return LLMK_ERR_ALIGNMENT;
+  return rope_vec_launch<true>(
+      reinterpret_cast<f16*>(q), const_cast<f16*>(reinterpret_cast<const f16*>(k)),
+      reinterpret_cast<const f16*>(v), reinterpret_cast<f16*>(k_pool),
+      reinterpret_cast<f16*>(v_pool), block_tables, positions, inv_freq, n, n_heads, n_kv_heads,
+      head_dim, max_pages, page_size, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,189 @@
+"""Seeded synthetic workloads of the benchmark configurations, built directly in device memory,
+and the algorithmic byte count of each kernel (bytes that must cross HBM once: inputs read
+once, outputs written once).
+
+Shapes are Llama-3.2-1B's (ref: engine/layer.h:6-9, engine/model.cu:20): hidden 2048, 32 query
+heads, 8 KV heads, head_dim 64, MLP width 8192, vocab 128256, 16 layers, KV pages of 16 tokens
+in per-layer pools laid out [num_pages, page_size, n_kv_heads, head_dim] (ref:
+engine/paged.h:6-9) and filled with the fp16 NaN pattern 0x7F7F (ref: engine/paged.cu:22).
+
+Random data comes from torch's device generator (fp32 normal draws rounded to fp16); page
+assignment from a seeded numpy permutation, as the reference's paged tests shuffle their free
+list (ref: tests/test_generate_batched.cu:28-29).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+HIDDEN, N_HEADS, N_KV, HEAD_DIM, INTER, VOCAB, LAYERS = 2048, 32, 8, 64, 8192, 128256, 16
+PAGE, EPS = 16, 1e-5
+ROPE_ARGS = (500000.0, 32.0, 1.0, 4.0, 8192.0)  # theta, factor, low, high, original max pos
+MAX_POS = 131072
+POISON = 0x7F7F
+SEED_BASE = 0x5EED0000
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def normal_f16(shape, g, device, mean=0.0, std=1.0) -> torch.Tensor:
+    t = torch.randn(shape, generator=g, device=device, dtype=torch.float32)
+    if std != 1.0:
+        t.mul_(std)
+    if mean != 0.0:
+        t.add_(mean)
+    return t.to(torch.float16)
+
+
+def poisoned(numel: int, device) -> torch.Tensor:
+    return torch.full((numel,), POISON, dtype=torch.int16, device=device).view(torch.float16)
+
+
+# ---------------------------------------------------------------------------------------------
+# algorithmic bytes per launch
+# ---------------------------------------------------------------------------------------------
+def bytes_add_rmsnorm(rows: int, hidden: int) -> int:
+    return 4 * rows * hidden * 2 + hidden * 2  # read residual + x, write residual + out; w once
+
+
+def bytes_rmsnorm(rows: int, hidden: int) -> int:
+    return 2 * rows * hidden * 2 + hidden * 2
+
+
+def bytes_rope(T: int, nh: int, nkv: int, hd: int) -> int:
+    return 2 * T * (nh + nkv) * hd * 2 + T * 4 + hd // 2 * 4  # q, k in place; positions; table
+
+
+def bytes_swiglu(n: int) -> int:
+    return 3 * n * 2
+
+
+def bytes_embedding(n: int, hidden: int) -> int:
+    return n * 4 + 2 * n * hidden * 2  # ids; the gathered rows read once and written once
+
+
+def bytes_rope_kv_scatter(n: int, nh: int, nkv: int, hd: int) -> int:
+    q = 2 * n * nh * hd * 2           # q rotated in place
+    kv = 2 * 2 * n * nkv * hd * 2     # k and v read, their pool rows written
+    return q + kv + n * 4 + n * 4 + hd // 2 * 4  # positions, the one table entry each
+    # sequence's row address needs, the rotation table
+
+
+def bytes_decode_pass(n: int, layers: int) -> int:
+    per_layer = (bytes_add_rmsnorm(n, HIDDEN)
+                 + bytes_rope_kv_scatter(n, N_HEADS, N_KV, HEAD_DIM)
+                 + bytes_swiglu(n * INTER))
+    return bytes_embedding(n, HIDDEN) + layers * per_layer
+
+
+# ---------------------------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------------------------
+def add_rmsnorm_inputs(rows=8192, hidden=HIDDEN, seed=SEED_BASE + 2, device="cuda") -> dict:
+    g = _gen(seed, device)
+    return dict(residual=normal_f16((rows, hidden), g, device),
+                x=normal_f16((rows, hidden), g, device),
+                w=normal_f16((hidden,), g, device, 1.0, 0.1),
+                out=torch.empty((rows, hidden), dtype=torch.float16, device=device),
+                rows=rows, hidden=hidden, eps=EPS)
+
+
+def rope_inputs(T=8192, nh=N_HEADS, nkv=N_KV, hd=HEAD_DIM, seed=SEED_BASE + 3,
+                device="cuda", inv_freq=None) -> dict:
+    g = _gen(seed, device)
+    return dict(q=normal_f16((T, nh, hd), g, device), k=normal_f16((T, nkv, hd), g, device),
+                positions=torch.randint(0, MAX_POS, (T,), generator=g, device=device,
+                                        dtype=torch.int32),
+                inv_freq=inv_freq, T=T, nh=nh, nkv=nkv, hd=hd)
+
+
+def swiglu_inputs(rows=8192, inter=INTER, seed=SEED_BASE + 4, device="cuda") -> dict:
+    g = _gen(seed, device)
+    return dict(gate=normal_f16((rows, inter), g, device), up=normal_f16((rows, inter), g, device),
+                out=torch.empty((rows, inter), dtype=torch.float16, device=device),
+                n=rows * inter)
+
+
+def embedding_table(vocab=VOCAB, hidden=HIDDEN, seed=SEED_BASE + 40, device="cuda"):
+    return normal_f16((vocab, hidden), _gen(seed, device), device, 0.0, 0.02)
+
+
+def embedding_inputs(n=8192, table=None, seed=SEED_BASE + 41, device="cuda") -> dict:
+    if table is None:
+        table = embedding_table(device=device)
+    g = _gen(seed, device)
+    return dict(table=table,
+                ids=torch.randint(0, table.shape[0], (n,), generator=g, device=device,
+                                  dtype=torch.int32),
+                out=torch.empty((n, table.shape[1]), dtype=torch.float16, device=device),
+                n=n, hidden=table.shape[1])
+
+
+@dataclass
+class DecodePassInputs:
+    """Config 5: one non-GEMM decode step for n sequences over `layers` layers."""
+    n: int
+    layers: int
+    max_pages: int
+    total_pages: int
+    lens: np.ndarray             # context lengths L_b (host)
+    tables_host: np.ndarray      # [n, max_pages] int32
+    table: torch.Tensor          # embedding table [vocab, hidden]
+    token_ids: torch.Tensor      # [n]
+    residual: torch.Tensor       # [n, hidden]
+    block_tables: torch.Tensor   # [n, max_pages]
+    positions: torch.Tensor      # [n] = L_b - 1
+    inv_freq: torch.Tensor       # [hd/2]
+    per_layer: list = field(default_factory=list)  # dicts for llmk.DecodeNonGemmPass
+
+    def pool_rows(self) -> np.ndarray:
+        """Pool row written for each sequence (host)."""
+        pos = self.lens - 1
+        return (self.tables_host[np.arange(self.n), pos // PAGE] * PAGE + pos % PAGE).astype(
+            np.int64)
+
+
+def decode_pass_inputs(inv_freq: torch.Tensor, n=256, layers=LAYERS, max_pages=128,
+                       table=None, seed=SEED_BASE + 5, device="cuda") -> DecodePassInputs:
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1, max_pages * PAGE + 1, n)
+    npages = (lens + PAGE - 1) // PAGE
+    total = int(npages.sum())
+    perm = rng.permutation(total).astype(np.int32)
+    tables = np.zeros((n, max_pages), np.int32)
+    off = 0
+    for b, p in enumerate(npages):
+        tables[b, :p] = perm[off:off + p]
+        off += p
+    g = _gen(seed, device)
+    if table is None:
+        table = embedding_table(device=device)
+    ids = torch.randint(0, table.shape[0], (n,), generator=g, device=device, dtype=torch.int32)
+    kvdim = N_KV * HEAD_DIM
+    per_layer = []
+    for _ in range(layers):
+        per_layer.append(dict(
+            x=normal_f16((n, HIDDEN), g, device),
+            norm_w=normal_f16((HIDDEN,), g, device, 1.0, 0.1),
+            normed=torch.empty((n, HIDDEN), dtype=torch.float16, device=device),
+            q=normal_f16((n, N_HEADS, HEAD_DIM), g, device),
+            k=normal_f16((n, N_KV, HEAD_DIM), g, device),
+            v=normal_f16((n, N_KV, HEAD_DIM), g, device),
+            k_pool=poisoned(total * PAGE * kvdim, device),
+            v_pool=poisoned(total * PAGE * kvdim, device),
+            gate=normal_f16((n, INTER), g, device),
+            up=normal_f16((n, INTER), g, device),
+            act=torch.empty((n, INTER), dtype=torch.float16, device=device)))
+    return DecodePassInputs(
+        n=n, layers=layers, max_pages=max_pages, total_pages=total, lens=lens,
+        tables_host=tables, table=table, token_ids=ids,
+        residual=torch.empty((n, HIDDEN), dtype=torch.float16, device=device),
+        block_tables=torch.from_numpy(tables).to(device),
+        positions=torch.from_numpy((lens - 1).astype(np.int32)).to(device),
+        inv_freq=inv_freq, per_layer=per_layer)

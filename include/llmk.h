@@ -1,0 +1,170 @@
+/*
+ * llmk.h - C-ABI of libllmk, the MI355X (gfx950) implementation of the non-GEMM layer kernels
+ * of a Llama-style fp16 decoder: embedding gather, residual add, RMSNorm, fused residual add +
+ * RMSNorm, RoPE with Llama-3 frequency scaling, SwiGLU, and the paged KV scatter (plain and
+ * fused with RoPE).
+ *
+ * Conventions shared by every entry point:
+ *  - Tensors are device pointers owned by the caller; fp16 values travel as uint16_t bit
+ *    patterns, indices as int32_t. Nothing is allocated and no state is kept between calls.
+ *  - `stream` is a hipStream_t (NULL = the null stream). Work is enqueued, never waited for.
+ *  - The return value is LLMK_OK (0), a hipError_t value from the launch, or one of the
+ *    LLMK_ERR_* codes below for an argument that violates a precondition (then nothing is
+ *    enqueued). llmk_error_string() names either kind.
+ *  - A zero element/row/token count is a no-op that returns LLMK_OK.
+ *  - Functions are re-entrant; different host threads may call them on different streams.
+ *
+ * Citations "ref: file:line" point into JayeshNikam36/cuda-llm-engine, whose free C++ launchers
+ * these entry points replace one for one (names, argument order and meaning kept; __half* ->
+ * uint16_t*, cudaStream_t -> void*, void -> status code). include/llmk.hpp restores the
+ * reference's exact C++ signatures on top of this header.
+ */
+#ifndef LLMK_H
+#define LLMK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define LLMK_API __attribute__((visibility("default")))
+#else
+#define LLMK_API
+#endif
+
+/* Status codes that are not hipError_t values. */
+#define LLMK_OK 0
+#define LLMK_ERR_INVALID_VALUE 10001 /* negative size, NULL pointer with a nonzero size */
+#define LLMK_ERR_SHAPE 10002         /* size not a multiple the layout requires */
+#define LLMK_ERR_ALIGNMENT 10003     /* a pointer that must be 16-byte aligned is not */
+#define LLMK_ERR_UNSUPPORTED 10004   /* a shape outside what the kernels implement */
+
+/* Human-readable name of a status code (LLMK_ERR_* or hipError_t). Never NULL. */
+LLMK_API const char* llmk_error_string(int status);
+
+/* Library version, major * 10000 + minor * 100 + patch. */
+LLMK_API int llmk_version(void);
+
+/* out[t, :] = table[ids[t], :] for t < n_tokens; bit-exact copy of hidden fp16 values per row.
+ * hidden % 8 == 0; table and out 16-byte aligned. ids are not range-checked (as in the
+ * reference): every id must lie in [0, rows of table).
+ * ref: kernels/embedding.cuh:6-7, kernels/embedding.cu:4-16 (embedding_lookup). */
+LLMK_API int llmk_embedding_lookup(const uint16_t* table, const int32_t* ids, uint16_t* out,
+                          int n_tokens, int hidden, void* stream);
+
+/* out[i] = fp16_rne(float(a[i]) + float(b[i])) for i < n. out may be the same pointer as a or
+ * b (in place); any alignment and any n are accepted.
+ * ref: kernels/residual_add.cuh:5-6, kernels/residual_add.cu:5-18 (residual_add). */
+LLMK_API int llmk_residual_add(const uint16_t* a, const uint16_t* b, uint16_t* out, size_t n,
+                      void* stream);
+
+/* Per row r < n_rows of width hidden: ss = sum of float(x)^2 in fp32; inv = 1 / sqrt(ss/hidden +
+ * eps); out = fp16(float(w) * r16(float(x) * inv)) where r16 rounds to fp16 and back.
+ * hidden % 8 == 0; x, w, out 16-byte aligned.
+ * ref: kernels/rmsnorm.cuh:5-7, kernels/rmsnorm.cu:9-68 (rmsnorm). */
+LLMK_API int llmk_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int n_rows, int hidden,
+                 float eps, void* stream);
+
+/* Fused residual add + RMSNorm: residual <- fp16(residual + x) in place (bit-exact, the same
+ * value llmk_residual_add writes), then out = rmsnorm(residual) as llmk_rmsnorm.
+ * Replaces the residual_add -> rmsnorm pairs at ref: engine/batched.cu:64->66 and :71->:51
+ * (engine/layer.cu:76->79, :84->69). New entry point; no single reference function. */
+LLMK_API int llmk_add_rmsnorm(uint16_t* residual, const uint16_t* x, const uint16_t* w, uint16_t* out,
+                     int n_rows, int hidden, float eps, void* stream);
+
+/* Host function: the head_dim/2 rotation speeds with Llama-3 frequency scaling, computed in
+ * fp32 step by step, written to out[0 .. head_dim/2). head_dim even and > 0.
+ * ref: kernels/rope.cuh:7-9, kernels/rope.cu:4-23 (compute_rope_inv_freq). */
+LLMK_API int llmk_compute_rope_inv_freq(int head_dim, double theta, double factor,
+                               double low_freq_factor, double high_freq_factor,
+                               double original_max_pos, float* out);
+
+/* In-place rotary embedding of q [n_tokens, n_heads, head_dim] and k [n_tokens, n_kv_heads,
+ * head_dim]; element i is paired with i + head_dim/2. For angle a = float(pos[t]) * inv_freq[i]
+ * (fp32 product): c = r16(cos a), s = r16(sin a); x1' = fp16(r16(x1*c) - r16(x2*s)),
+ * x2' = fp16(r16(x2*c) + r16(x1*s)). inv_freq is a device pointer to head_dim/2 floats.
+ * head_dim even; q and k 16-byte aligned when head_dim % 16 == 0 (the vector path).
+ * ref: kernels/rope.cuh:11-15, kernels/rope.cu:24-49 (rope_apply). */
+LLMK_API int llmk_rope_apply(uint16_t* q, uint16_t* k, const int32_t* positions, const float* inv_freq,
+                    int n_tokens, int n_heads, int n_kv_heads, int head_dim, void* stream);
+
+/* out[i] = fp16(r16(g / (1 + exp(-g))) * float(up[i])) with g = float(gate[i]), for i < n.
+ * Any alignment and any n are accepted.
+ * ref: kernels/swiglu.cuh:5-6, kernels/swiglu.cu:4-21 (swiglu). */
+LLMK_API int llmk_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n,
+                void* stream);
+
+/* Prefill scatter: for t < T, pos = start_pos + t, row = block_table[pos / page_size] *
+ * page_size + pos % page_size, pool[row*kvdim .. +kvdim) = src[t*kvdim .. +kvdim). Pool layout
+ * [num_pages, page_size, n_kv_heads, head_dim]. kvdim % 8 == 0; src and pool 16-byte aligned.
+ * Page numbers are not range-checked (as in the reference).
+ * ref: kernels/kv_scatter.cuh:5-8, kernels/kv_scatter.cu:4-12,26-32 (kv_scatter). */
+LLMK_API int llmk_kv_scatter(const uint16_t* src, uint16_t* pool, const int32_t* block_table,
+                    int start_pos, int T, int page_size, int kvdim, void* stream);
+
+/* Decode scatter: for b < n, row = block_tables[b*max_pages + pos[b]/page_size] * page_size +
+ * pos[b] % page_size; pool[row*kvdim .. +kvdim) = src[b*kvdim .. +kvdim).
+ * kvdim % 8 == 0; src and pool 16-byte aligned.
+ * ref: kernels/kv_scatter.cuh:10-13, kernels/kv_scatter.cu:14-24,34-40 (kv_scatter_batch). */
+LLMK_API int llmk_kv_scatter_batch(const uint16_t* src, uint16_t* pool, const int32_t* block_tables,
+                          const int32_t* positions, int n, int max_pages, int page_size,
+                          int kvdim, void* stream);
+
+/* Fused decode RoPE + KV scatter, one new token per sequence b < n at position positions[b]:
+ * q [n, n_heads, head_dim] is rotated in place (as llmk_rope_apply); k [n, n_kv_heads,
+ * head_dim] is rotated (as llmk_rope_apply) and written to k_pool at the llmk_kv_scatter_batch
+ * address; v [n, n_kv_heads, head_dim] is copied bit-exact to v_pool at the same address. k and
+ * v are only read. head_dim % 16 == 0; q, k, v, k_pool, v_pool 16-byte aligned.
+ * Replaces ref: engine/batched.cu:55-58 (rope_apply, then kv_scatter_batch for K and V). New
+ * entry point; no single reference function. */
+LLMK_API int llmk_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               uint16_t* k_pool, uint16_t* v_pool, const int32_t* block_tables,
+                               const int32_t* positions, const float* inv_freq, int n,
+                               int max_pages, int page_size, int n_heads, int n_kv_heads,
+                               int head_dim, void* stream);
+
+/* Device-to-device copy of nbytes with 16-byte vector loads and stores, used to measure the
+ * practical HBM ceiling and to calibrate rocprof traffic counters. src and dst 16-byte aligned,
+ * nbytes % 16 == 0. ref: bench/bandwidth.cu:11-15 (copy_vec4, the reference's bandwidth probe). */
+LLMK_API int llmk_copy_bytes(const void* src, void* dst, size_t nbytes, void* stream);
+
+/* One non-GEMM decode-step pass: the embedding gather into `residual`, then per layer l the
+ * operations the reference's batched layer issues between its GEMMs and attention
+ * (ref: engine/batched.cu:51-71, :112-115): add+RMSNorm of residual with x[l] (out normed[l]),
+ * RoPE of q[l] / k[l] with the scatter of k[l] and v[l] into k_pool[l] / v_pool[l], and SwiGLU
+ * of gate[l], up[l] into act[l]. The per-layer arrays are HOST arrays of n_layers device
+ * pointers. Every launch goes to `stream` in that order, so the pass can be captured into a
+ * HIP graph. */
+typedef struct llmk_decode_pass {
+  int n_seqs, n_layers, hidden, n_heads, n_kv_heads, head_dim, inter;
+  int page_size, max_pages;
+  float eps;
+  const uint16_t* embed_table; /* [vocab, hidden] */
+  const int32_t* token_ids;    /* [n_seqs] */
+  uint16_t* residual;          /* [n_seqs, hidden]: embedding output, then the residual chain */
+  const int32_t* block_tables; /* [n_seqs, max_pages] */
+  const int32_t* positions;    /* [n_seqs] */
+  const float* inv_freq;       /* [head_dim / 2] */
+  const uint16_t* const* x;        /* per layer [n_seqs, hidden]: added into residual */
+  const uint16_t* const* norm_w;   /* per layer [hidden] */
+  uint16_t* const* normed;         /* per layer [n_seqs, hidden] */
+  uint16_t* const* q;              /* per layer [n_seqs, n_heads, head_dim], rotated in place */
+  const uint16_t* const* k;        /* per layer [n_seqs, n_kv_heads, head_dim] */
+  const uint16_t* const* v;        /* per layer [n_seqs, n_kv_heads, head_dim] */
+  uint16_t* const* k_pool;         /* per layer [num_pages, page_size, n_kv_heads, head_dim] */
+  uint16_t* const* v_pool;         /* per layer, same layout */
+  const uint16_t* const* gate;     /* per layer [n_seqs, inter] */
+  const uint16_t* const* up;       /* per layer [n_seqs, inter] */
+  uint16_t* const* act;            /* per layer [n_seqs, inter] */
+} llmk_decode_pass;
+
+LLMK_API int llmk_decode_nongemm_pass(const llmk_decode_pass* pass, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* LLMK_H */

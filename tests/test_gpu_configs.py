@@ -1,0 +1,190 @@
+"""GPU parity at the benchmark configurations' full sizes (the oracle finishes each in seconds),
+the 16-layer decode-step pass (config 5) checked layer by layer, HIP-graph replay of that pass,
+and the engine-style C++ drop-in test."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import EPS, POISON, ROPE, assert_tol
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def host_i32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy().astype(np.int32)
+
+
+@pytest.fixture(scope="module")
+def wl(llmk):
+    import llmk.workloads as w
+    return w
+
+
+@pytest.fixture(scope="module")
+def inv(llmk, orc):
+    hd = 64
+    inv_h = orc.compute_rope_inv_freq(hd, ROPE["theta"], ROPE["factor"], ROPE["low"],
+                                      ROPE["high"], ROPE["orig"])
+    inv_lib = np.array(llmk.compute_rope_inv_freq(hd, ROPE["theta"], ROPE["factor"], ROPE["low"],
+                                                  ROPE["high"], ROPE["orig"]), np.float32)
+    assert np.array_equal(inv_h.view(np.uint32), inv_lib.view(np.uint32))
+    return inv_h, torch.from_numpy(inv_lib).to(DEV)
+
+
+def test_config1_rmsnorm_16x2048(llmk, orc, wl):
+    d = wl.add_rmsnorm_inputs(rows=16, seed=wl.SEED_BASE + 1)
+    llmk.rmsnorm(d["x"], d["w"], d["out"], 16, 2048, EPS)
+    exp = orc.rmsnorm(host(d["x"]), host(d["w"]), 16, 2048, EPS)
+    assert_tol(orc.compare(host(d["out"]), exp), 0.99, "config 1")
+
+
+def test_config2_add_rmsnorm_8192x2048(llmk, orc, wl):
+    d = wl.add_rmsnorm_inputs()
+    r, x, w = host(d["residual"]), host(d["x"]), host(d["w"])
+    llmk.add_rmsnorm(d["residual"], d["x"], d["w"], d["out"], d["rows"], d["hidden"], EPS)
+    o_exp = orc.add_rmsnorm(r, x, w, d["rows"], d["hidden"], EPS, threads=THREADS)
+    assert np.array_equal(host(d["residual"]), r), "updated residual must be bit-exact"
+    cmp = orc.compare(host(d["out"]), o_exp)
+    print(f"config 2 out: {cmp}")
+    assert_tol(cmp, 0.99, "config 2")
+
+
+def test_config3_rope_8192_tokens(llmk, orc, wl, inv):
+    d = wl.rope_inputs(inv_freq=inv[1])
+    q, k, pos = host(d["q"]), host(d["k"]), host_i32(d["positions"])
+    assert pos.min() >= 0 and pos.max() < wl.MAX_POS
+    llmk.rope_apply(d["q"], d["k"], d["positions"], d["inv_freq"], d["T"], d["nh"], d["nkv"],
+                    d["hd"])
+    orc.rope_apply(q, k, pos, inv[0], d["T"], d["nh"], d["nkv"], d["hd"], threads=THREADS)
+    cq, ck = orc.compare(host(d["q"]), q), orc.compare(host(d["k"]), k)
+    print(f"config 3 Q: {cq}\nconfig 3 K: {ck}")
+    assert_tol(cq, 0.995, "config 3 Q")
+    assert_tol(ck, 0.995, "config 3 K")
+
+
+def test_config4_swiglu_8192x8192(llmk, orc, wl):
+    d = wl.swiglu_inputs()
+    g, u = host(d["gate"]), host(d["up"])
+    llmk.swiglu(d["gate"], d["up"], d["out"], d["n"])
+    cmp = orc.compare(host(d["out"]), orc.swiglu(g, u, threads=THREADS))
+    print(f"config 4 swiglu: {cmp}")
+    assert_tol(cmp, 0.995, "config 4")
+
+
+def test_config4_embedding_8192_of_128256(llmk, orc, wl):
+    d = wl.embedding_inputs()
+    llmk.embedding_lookup(d["table"], d["ids"], d["out"], d["n"], d["hidden"])
+    ids = host_i32(d["ids"])
+    table = host(d["table"]).reshape(-1, d["hidden"])
+    assert np.array_equal(host(d["out"]), orc.embedding_lookup(table, ids, d["hidden"],
+                                                               threads=THREADS))
+
+
+def _check_decode_pass(orc, wl, p, inv_h, expected_residual_in):
+    """Checks every layer of a finished pass against the oracle; returns the final residual."""
+    n, hidden, kvdim = p.n, wl.HIDDEN, wl.N_KV * wl.HEAD_DIM
+    rows = torch.from_numpy(p.pool_rows()).to(DEV)
+    pos = (p.lens - 1).astype(np.int32)
+    res = expected_residual_in.copy()
+    for l, L in enumerate(p.per_layer):
+        normed = orc.add_rmsnorm(res, host(L["x"]), host(L["norm_w"]), n, hidden, EPS)
+        assert_tol(orc.compare(host(L["normed"]), normed), 0.99, f"layer {l} normed")
+        q_e, k_e = host(L["q_in"]), host(L["k"])
+        orc.rope_apply(q_e, k_e, pos, inv_h, n, wl.N_HEADS, wl.N_KV, wl.HEAD_DIM)
+        assert_tol(orc.compare(host(L["q"]), q_e), 0.995, f"layer {l} q")
+        kp = L["k_pool"].view(-1, kvdim)
+        vp = L["v_pool"].view(-1, kvdim)
+        assert_tol(orc.compare(host(kp.index_select(0, rows)), k_e.reshape(n, kvdim)), 0.995,
+                   f"layer {l} K pool")
+        assert np.array_equal(host(vp.index_select(0, rows)), host(L["v"]).reshape(n, kvdim))
+        poison = torch.tensor(POISON, dtype=torch.int16, device=DEV)
+        for pool in (kp, vp):
+            changed = (pool.view(torch.int16) != poison).any(dim=1)
+            assert int(changed.sum()) == n, f"layer {l}: rows outside the addressed slots changed"
+        act = orc.swiglu(host(L["gate"]), host(L["up"]), threads=THREADS)
+        assert_tol(orc.compare(host(L["act"]), act), 0.995, f"layer {l} act")
+    return res
+
+
+def test_config5_decode_pass_16_layers_256_seqs(llmk, orc, wl, inv):
+    p = wl.decode_pass_inputs(inv[1])
+    for L in p.per_layer:
+        L["q_in"] = L["q"].clone()
+    dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables, p.positions,
+                                p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
+                                n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
+                                page_size=wl.PAGE, max_pages=p.max_pages, eps=EPS)
+    dp.run()
+    torch.cuda.synchronize()
+    ids = host_i32(p.token_ids)
+    emb = host(p.table.index_select(0, p.token_ids.long()))
+    assert np.array_equal(emb, host(p.table).reshape(-1, wl.HIDDEN)[ids])
+    final = _check_decode_pass(orc, wl, p, inv[0], emb)
+    assert np.array_equal(host(p.residual), final), "residual chain must be bit-exact"
+
+
+def test_decode_pass_hip_graph_replays(llmk, orc, wl, inv):
+    """The pass captured into a HIP graph (through torch.cuda.CUDAGraph) and replayed three
+    times, with eager work and synchronisation between replays, gives the eager result each
+    time."""
+    p = wl.decode_pass_inputs(inv[1], n=64, layers=3, max_pages=32, seed=wl.SEED_BASE + 55)
+    state0 = [(L["q"].clone(), L["k_pool"].clone(), L["v_pool"].clone()) for L in p.per_layer]
+    dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables, p.positions,
+                                p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
+                                n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
+                                page_size=wl.PAGE, max_pages=p.max_pages, eps=EPS)
+
+    def reset():
+        for L, (q0, kp0, vp0) in zip(p.per_layer, state0):
+            L["q"].copy_(q0)
+            L["k_pool"].copy_(kp0)
+            L["v_pool"].copy_(vp0)
+            L["normed"].zero_()
+            L["act"].zero_()
+        p.residual.zero_()
+
+    def snapshot():
+        torch.cuda.synchronize()
+        outs = [host(p.residual)]
+        for L in p.per_layer:
+            outs += [host(L[k]) for k in ("normed", "q", "k_pool", "v_pool", "act")]
+        return outs
+
+    dp.run()
+    eager = snapshot()
+    reset()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        dp.run()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dp.run()
+    for i in range(3):
+        reset()
+        torch.cuda.synchronize()
+        _ = torch.randn(1 << 20, device=DEV).sum().item()  # unrelated eager work in between
+        graph.replay()
+        got = snapshot()
+        for j, (a, b) in enumerate(zip(got, eager)):
+            assert np.array_equal(a, b), f"replay {i}, output {j} differs from the eager pass"
+
+
+def test_cpp_dropin_binary():
+    """Engine-style C++ through llmk.hpp (the reference's launcher names and argument lists)."""
+    exe = os.path.join(ROOT, "tests", "cpp", "llmk_dropin_test")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=100)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "ALL PASSED" in r.stdout
