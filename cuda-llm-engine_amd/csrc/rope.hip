@@ -8,8 +8,8 @@
 // two fp16 values rounded to fp16, which the packed fp16 instructions compute bit for bit.
 //
 // Work split: a block owns `tpb` consecutive tokens. Phase 1 computes the tpb * head_dim/2 (cos,
-// sin) pairs once each with the full-range sincosf and keeps them in LDS as fp16 (the reference
-// evaluates sincosf once per head, 40x as often). Phase 2 walks the (token, head, j) tasks: a
+// sin) pairs once each and keeps them in LDS as fp16 (the reference evaluates sincosf once per
+// head, 40x as often). Phase 2 walks the (token, head, j) tasks: a
 // task loads the 16-byte vector j of the first half of one head row and vector j of the second
 // half, which hold exactly the 8 pairs (8j .. 8j+7, +head_dim/2), rotates them with four packed
 // multiplies and two packed adds per 2 values, and stores both vectors. Q and K rows are read
@@ -38,6 +38,20 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
   return (__umulhi(n, f.m) + n) >> f.s;
 }
 
+// cos and sin of the fp32 angle `a`, rounded to fp16. They are evaluated in fp64 (OCML sincos,
+// full-range argument reduction) and rounded fp64 -> fp32 -> fp16, so the fp16 values are the
+// roundings of the fp32 roundings of the exact results except in vanishingly rare ties. The
+// angles reach 131071 rad; an fp32 sincos with a last-bit error can move c or s by one fp16 ulp,
+// and x1*c - x2*s then cancels to a value with a large relative error. 32 evaluations per
+// token, shared by all of its heads, keep the fp64 cost off the critical path.
+__device__ __forceinline__ void cos_sin_f16(float a, f16* c, f16* s) {
+  double sd, cd;
+  sincos((double)a, &sd, &cd);
+  const float cf = (float)cd, sf = (float)sd;
+  *c = (f16)cf;
+  *s = (f16)sf;
+}
+
 // HV = 16-byte vectors per half head row (head_dim = 16 * HV).
 template <int HV, bool FUSED>
 __global__ void __launch_bounds__(256)
@@ -55,11 +69,7 @@ k_rope_vec(f16* q, f16* k, const f16* __restrict__ v, f16* k_pool, f16* v_pool,
 
   for (int e = threadIdx.x; e < ntok * HALF; e += blockDim.x) {
     const int tt = e / HALF, i = e % HALF;
-    const float a = (float)pos[t0 + tt] * inv_freq[i];
-    float sn, cn;
-    sincosf(a, &sn, &cn);
-    cs[tt * HD + i] = (f16)cn;
-    cs[tt * HD + HALF + i] = (f16)sn;
+    cos_sin_f16((float)pos[t0 + tt] * inv_freq[i], cs + tt * HD + i, cs + tt * HD + HALF + i);
   }
   if (FUSED) {
     for (int tt = threadIdx.x; tt < ntok; tt += blockDim.x) {
@@ -119,11 +129,7 @@ k_rope_scalar(f16* q, f16* k, const int* __restrict__ pos, const float* __restri
   const int ntok = min(tpb, n_tokens - t0);
   for (int e = threadIdx.x; e < ntok * half; e += blockDim.x) {
     const int tt = e / half, i = e % half;
-    const float a = (float)pos[t0 + tt] * inv_freq[i];
-    float sn, cn;
-    sincosf(a, &sn, &cn);
-    cs[tt * hd + i] = (f16)cn;
-    cs[tt * hd + half + i] = (f16)sn;
+    cos_sin_f16((float)pos[t0 + tt] * inv_freq[i], cs + tt * hd + i, cs + tt * hd + half + i);
   }
   __syncthreads();
   const int per_tok = (nh + nkv) * half;

@@ -65,7 +65,7 @@ static bool within_tol(const std::vector<uint16_t>& got, const std::vector<uint1
     const double g = or_h2f(got[i]), e = or_h2f(exp[i]), d = std::fabs(g - e);
     exact += got[i] == exp[i];
     max_abs = std::max(max_abs, d);
-    if (!(d <= 1e-3 + 4e-3 * std::fabs(e))) ++bad;
+    if (got[i] != exp[i] && !(d <= 1e-3 + 4e-3 * std::fabs(e))) ++bad;  // NaN poison: bits
   }
   std::snprintf(detail, dlen, "(max_abs %.2e, exact %.3f%%)", max_abs,
                 100.0 * exact / std::max<size_t>(1, got.size()));
