@@ -12,9 +12,11 @@ Caches: MI355X has a 256 MB Infinity Cache (MALL) in front of HBM and 4 MB of L2
 kernel cycles through enough independent input sets that the data of a launch was last
 touched more than 1 GB of traffic earlier, so it cannot be served from the MALL.
 
-Timing: every launch is bracketed by HIP events recorded on the stream it is launched on
-(torch's current stream); `roofline.achieved` = algorithmic bytes / mean event time of one
-launch. `ms_per_step` = wall time of the K timed steps (synchronised on both sides) / K.
+Timing: `ms_per_step` = host wall time of K back-to-back steps, synchronised on both sides, / K;
+`value` = algorithmic bytes per step / ms_per_step. Then K more launches are enqueued behind a
+short spin kernel with a HIP event right before the first and right after the last, recorded on
+the stream they are launched on (torch's current stream); the mean launch duration is the event
+interval / K, and `roofline.achieved` = algorithmic bytes / that mean.
 
 CPU baseline: the scalar C oracle of the same op (oracle/, test infrastructure) on the host's
 cores, over a bounded sample of the same workload.
@@ -33,7 +35,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = ("achieved HBM GB/s (% of ~8 TB/s) per fused kernel; "
           "µs per 16-layer non-GEMM pass")
 PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_counters.txt")
+WARM_S = 0.25
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "nongemm_kernels_counters_traffic.txt")
 
 
 def log(msg: str) -> None:
@@ -48,6 +51,8 @@ def parse_args():
     ap.add_argument("--kernels", choices=["all", "headline"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
+                    help="summarise rocprofv3 csv output of this bench instead of running it")
     return ap.parse_args()
 
 
@@ -65,44 +70,154 @@ def read_traffic() -> dict:
     return out
 
 
+
+# (label, kernel-name substring, grid size in work-items, algorithmic bytes) of each measured
+# launch shape; grid sizes follow from the launchers' grid choices at the benchmark shapes.
+PROFILE_SHAPES = [
+    ("add_rmsnorm_8192x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 8192 * 64, 134221824),
+    ("rmsnorm_16x2048", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
+    ("rope_8192", "k_rope_vecILi4ELi12ELb0E", 1024 * 256, 83918976),
+    ("swiglu_8192x8192", "k_swiglu_vecILi2E", 16384 * 256, 402653184),
+    ("embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
+    ("copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),
+    ("decode:embedding_256", "k_embeddingILi0E", 256 * 64, 2098176),
+    ("decode:add_rmsnorm_256x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 256 * 64, 4198400),
+    ("decode:rope_kv_scatter_256", "k_rope_vecILi4ELi2ELb1E", 256 * 256, 3147904),
+    ("decode:swiglu_256x8192", "k_swiglu_vecILi2E", 512 * 256, 12582912),
+]
+
+
+def summarize_profiles(trace_dir, fetch_dir, write_dir):
+    """Per launch shape: mean kernel duration from the kernel trace, FETCH_SIZE and WRITE_SIZE per
+    dispatch, and HBM traffic per launch with each counter scaled by what it reads for the
+    1 GiB copy probe (1 GiB read, 1 GiB written)."""
+    import csv
+    import glob
+
+    def rows(d, suffix):
+        out = []
+        for f in glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True):
+            out += list(csv.DictReader(open(f)))
+        return out
+
+    def grid(r):
+        return int(r.get("Grid_Size_X") or r.get("Grid_Size"))
+
+    dur, cnt = {}, {}
+    for r in rows(trace_dir, "kernel_trace.csv"):
+        for label, name, g, _ in PROFILE_SHAPES:
+            if name in r["Kernel_Name"] and grid(r) == g:
+                dur.setdefault(label, []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+    for d, cname in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
+        for r in rows(d, "counter_collection.csv"):
+            if r["Counter_Name"] != cname:
+                continue
+            for label, name, g, _ in PROFILE_SHAPES:
+                if name in r["Kernel_Name"] and grid(r) == g:
+                    cnt.setdefault((label, cname), []).append(float(r["Counter_Value"]))
+    avg = {k: sum(v) / len(v) for k, v in cnt.items() if v}
+    copy_b = 1 << 30
+    sf = copy_b / (avg[("copy_1GiB", "FETCH_SIZE")] * 1024)
+    sw = copy_b / (avg[("copy_1GiB", "WRITE_SIZE")] * 1024)
+    print(f"# FETCH_SIZE scale {sf:.4f}, WRITE_SIZE scale {sw:.4f} "
+          f"(copy probe: 1 GiB read and 1 GiB written per launch)")
+    print("# label  us_mean  calls  fetch_kib  write_kib  traffic_bytes  algorithmic_bytes  ratio")
+    for label, _, _, alg in PROFILE_SHAPES:
+        d = dur.get(label, [])
+        f, w = avg.get((label, "FETCH_SIZE")), avg.get((label, "WRITE_SIZE"))
+        us = f"{sum(d) / len(d):.3f}" if d else "-"
+        if f is None or w is None:
+            print(f"{label} us_mean={us} calls={len(d)}")
+            continue
+        traffic = f * 1024 * sf + w * 1024 * sw
+        print(f"{label} us_mean={us} calls={len(d)} fetch_kib={f:.1f} write_kib={w:.1f} "
+              f"traffic_bytes={traffic:.0f} algorithmic_bytes={alg} ratio={traffic / alg:.4f}")
+
+
 class Timer:
-    """Per-launch HIP events on the launching stream plus host wall time over the region."""
+    """Two timed passes of `steps` launches each.
+
+    1. Host wall clock: `steps` back-to-back launches, torch.cuda.synchronize() on both sides.
+    2. HIP events: the stream is first held by a short spin kernel while filler launches (3 ms
+       of GPU time, to bring clocks back up) and then the `steps` timed launches are enqueued
+       behind it, with one event recorded right before the first timed launch and one right
+       after the last, on the launching stream. The mean launch duration is the event interval
+       / steps: the GPU runs the launches back to back, so host-side enqueue time is excluded.
+    """
 
     def __init__(self, torch):
         self.torch = torch
+        self.cycles_per_s = None
+
+    def _calibrate(self):
+        torch = self.torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 1 << 22
+        torch.cuda._sleep(n)  # warm the spin kernel
+        a.record()
+        torch.cuda._sleep(n)
+        b.record()
+        torch.cuda.synchronize()
+        self.cycles_per_s = n / max(a.elapsed_time(b) * 1e-3, 1e-9)
 
     def run(self, launch, n_sets: int, steps: int, warmup: int):
         torch = self.torch
-        for i in range(warmup):
+        if self.cycles_per_s is None:
+            self._calibrate()
+        # Warm-up: at least `warmup` launches and at least WARM_S seconds of back-to-back
+        # launches, so that clocks have ramped up from the idle state before timing starts
+        # (the first milliseconds after idle measured up to 15% slow).
+        t_w = time.perf_counter()
+        i = 0
+        while i < warmup or time.perf_counter() - t_w < WARM_S:
             launch(i % n_sets)
+            i += 1
+            if i % 64 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
-        stream = torch.cuda.current_stream()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
+        warmup = i
         t0 = time.perf_counter()
         for i in range(steps):
-            ev[i][0].record(stream)
             launch((warmup + i) % n_sets)
-            ev[i][1].record(stream)
+        enq = (time.perf_counter() - t0) / steps  # host time to enqueue one launch
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        per = [a.elapsed_time(b) * 1e-3 for a, b in ev]  # seconds
-        per.sort()
-        return {"wall_s": wall, "mean_s": sum(per) / len(per), "median_s": per[len(per) // 2],
-                "min_s": per[0]}
+
+        # Event pass. The stream is held by a spin kernel while everything is enqueued; behind
+        # it, `fill` launches of the same kernel (at least 3 ms of GPU time) bring the clocks
+        # back up from the spin kernel's idle load before the start event.
+        stream = torch.cuda.current_stream()
+        fill = min(4000, max(8, int(3e-3 / max(wall / steps, 1e-7))))
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        hold = max(2e-3, 3 * enq * (fill + steps))
+        torch.cuda._sleep(int(hold * self.cycles_per_s))
+        t1 = time.perf_counter()
+        for i in range(fill):
+            launch(i % n_sets)
+        a.record(stream)
+        for i in range(steps):
+            launch((warmup + steps + i) % n_sets)
+        b.record(stream)
+        enqueue = time.perf_counter() - t1
+        torch.cuda.synchronize()
+        ev = a.elapsed_time(b) * 1e-3
+        return {"wall_s": wall, "mean_s": ev / steps, "event_s": ev, "enqueue_s": enqueue,
+                "hold_s": hold, "queue_prefilled": enqueue < hold, "steps": steps}
 
 
 def kernel_entry(name, nbytes, t, traffic=None, extra=None):
     achieved = nbytes / t["mean_s"] / 1e9
     e = {"bytes": nbytes, "us_mean": round(t["mean_s"] * 1e6, 3),
-         "us_median": round(t["median_s"] * 1e6, 3), "us_min": round(t["min_s"] * 1e6, 3),
-         "GBps": round(achieved, 1), "frac_of_peak": round(achieved / PEAK_GBS, 4)}
+         "us_wall_per_step": round(t["wall_s"] / max(1, t.get("steps", 1)) * 1e6, 3),
+         "GBps": round(achieved, 1), "frac_of_peak": round(achieved / PEAK_GBS, 4),
+         "queue_prefilled": t["queue_prefilled"]}
     if traffic is not None:
         e["traffic_bytes"] = traffic
     if extra:
         e.update(extra)
     log(f"  {name:34s} {e['us_mean']:9.2f} us  {e['GBps']:8.1f} GB/s  "
-        f"{100 * e['frac_of_peak']:5.1f}% of 8 TB/s")
+        f"{100 * e['frac_of_peak']:5.1f}% of 8 TB/s  (wall {e['us_wall_per_step']:.2f} us/step)")
     return e
 
 
@@ -112,6 +227,9 @@ def sets_for(bytes_per_set: int, floor: int = 1 << 30, most: int = 64) -> int:
 
 def main() -> int:
     args = parse_args()
+    if args.summarize_profiles:
+        summarize_profiles(*args.summarize_profiles)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the kernels are single-GPU; this build has no "
               f"multi-GPU path): --gpus {args.gpus} is not supported", file=sys.stderr)
@@ -147,7 +265,7 @@ def main() -> int:
         llmk.add_rmsnorm(s["residual"], s["x"], w, s["out"], rows, hidden, wl.EPS)
 
     t = timer.run(launch_add_rmsnorm, R, K, W)
-    head = kernel_entry("add_rmsnorm [8192,2048]", nbytes, t, traffic.get("add_rmsnorm"),
+    head = kernel_entry("add_rmsnorm [8192,2048]", nbytes, t, traffic.get("add_rmsnorm_8192x2048"),
                         {"sets": R})
     kernels["add_rmsnorm_8192x2048"] = head
     headline_wall = t["wall_s"]
@@ -163,7 +281,7 @@ def main() -> int:
                                              hidden, wl.EPS), 8, K, W)
         kernels["rmsnorm_16x2048"] = kernel_entry("rmsnorm [16,2048]",
                                                   wl.bytes_rmsnorm(16, hidden), t,
-                                                  traffic.get("rmsnorm_16"))
+                                                  traffic.get("rmsnorm_16x2048"))
         del sets1
 
         # config 3: RoPE, Q [8192,32,64] + K [8192,8,64], positions < 131072
@@ -178,7 +296,7 @@ def main() -> int:
                                                 wl.N_KV, wl.HEAD_DIM), R3, K, W)
         kernels["rope_8192"] = kernel_entry(
             "rope_apply Q+K [8192 tokens]", wl.bytes_rope(T, wl.N_HEADS, wl.N_KV, wl.HEAD_DIM),
-            t, traffic.get("rope"), {"sets": R3})
+            t, traffic.get("rope_8192"), {"sets": R3})
         del sets3
 
         # config 4a: SwiGLU [8192, 8192]
@@ -188,7 +306,7 @@ def main() -> int:
         t = timer.run(lambda i: llmk.swiglu(sets4[i]["gate"], sets4[i]["up"], sets4[i]["out"], n),
                       R4, K, W)
         kernels["swiglu_8192x8192"] = kernel_entry("swiglu [8192,8192]", wl.bytes_swiglu(n), t,
-                                                   traffic.get("swiglu"), {"sets": R4})
+                                                   traffic.get("swiglu_8192x8192"), {"sets": R4})
         del sets4
         torch.cuda.empty_cache()
 
@@ -203,7 +321,7 @@ def main() -> int:
                                                       check_indices=False), R5, K, W)
         kernels["embedding_8192"] = kernel_entry(
             "embedding_lookup 8192 of 128256", wl.bytes_embedding(8192, hidden), t,
-            traffic.get("embedding"), {"sets": R5, "tables": 4,
+            traffic.get("embedding_8192"), {"sets": R5, "tables": 4,
                                        "note": "ids uniform; ~3% duplicate rows per launch"})
         table = tables[0]
         del sets5, tables
@@ -239,7 +357,7 @@ def main() -> int:
         t = timer.run(lambda i: llmk.copy_bytes(bufs[2 * (i % 2)], bufs[2 * (i % 2) + 1], nb),
                       2, max(20, K // 4), 5)
         kernels["copy_1GiB"] = kernel_entry("copy probe 1 GiB", 2 * nb, t,
-                                            traffic.get("copy"))
+                                            traffic.get("copy_1GiB"))
         del bufs
 
     # ---------------- CPU baseline: the scalar oracle on the host cores ----------------
@@ -258,7 +376,7 @@ def main() -> int:
                    "input_sets": head["sets"], "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["GBps"] / PEAK_GBS, 4),
-                     "traffic": traffic.get("add_rmsnorm")},
+                     "traffic": traffic.get("add_rmsnorm_8192x2048")},
         "cpu_baseline": cpu,
         "kernels": kernels,
     }

@@ -122,7 +122,7 @@ def _fail(fn: str, msg: str):
 def _dev(fn: str, t: torch.Tensor, dtype: torch.dtype, min_numel: int, name: str) -> int:
     if not isinstance(t, torch.Tensor):
         _fail(fn, f"{name} must be a torch tensor")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         _fail(fn, f"{name} must be a CUDA tensor, got {t.device}")
     if t.dtype != dtype:
         _fail(fn, f"{name} must be {dtype}, got {t.dtype}")
@@ -135,7 +135,7 @@ def _dev(fn: str, t: torch.Tensor, dtype: torch.dtype, min_numel: int, name: str
 
 def _stream(stream) -> int:
     if stream is None:
-        return torch.cuda.current_stream().cuda_stream
+        return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device())
     if isinstance(stream, torch.cuda.Stream):
         return stream.cuda_stream
     return int(stream)

@@ -13,7 +13,10 @@
 
 namespace llmk {
 
-template <int UNROLL>
+// Copies one row of vpr 16-byte vectors with one wave: lane l moves vectors l, l+64, ...;
+// UNROLL of them are loaded before any is stored. FULL: vpr is a multiple of 64 * UNROLL, so no
+// lane needs a bounds test.
+template <int UNROLL, bool FULL>
 __device__ __forceinline__ void copy_row(const f16* __restrict__ src, f16* __restrict__ dst,
                                          int vpr, int lane) {
   for (int v0 = 0; v0 < vpr; v0 += 64 * UNROLL) {
@@ -21,32 +24,86 @@ __device__ __forceinline__ void copy_row(const f16* __restrict__ src, f16* __res
 #pragma unroll
     for (int m = 0; m < UNROLL; ++m) {
       const int v = v0 + lane + 64 * m;
-      if (v < vpr) r[m] = ld16_stream(src + 8 * v);
+      if (FULL || v < vpr) r[m] = ld16_stream(src + 8 * v);
     }
 #pragma unroll
     for (int m = 0; m < UNROLL; ++m) {
       const int v = v0 + lane + 64 * m;
-      if (v < vpr) st16_stream(dst + 8 * v, r[m]);
+      if (FULL || v < vpr) st16_stream(dst + 8 * v, r[m]);
     }
   }
+}
+
+// 0: vpr a multiple of 256, 1: a multiple of 64, 2: anything.
+static int row_kind(int vpr) { return vpr % 256 == 0 ? 0 : (vpr % 64 == 0 ? 1 : 2); }
+
+template <int KIND>
+__device__ __forceinline__ void copy_row_kind(const f16* __restrict__ src, f16* __restrict__ dst,
+                                              int vpr, int lane) {
+  if (KIND == 0) copy_row<4, true>(src, dst, vpr, lane);
+  else if (KIND == 1) copy_row<1, true>(src, dst, vpr, lane);
+  else copy_row<4, false>(src, dst, vpr, lane);
 }
 
 __device__ __forceinline__ int wave_row() {
   return __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
 }
 
+template <int KIND>
 __global__ void __launch_bounds__(256)
 k_embedding(const f16* __restrict__ table, const int* __restrict__ ids, f16* __restrict__ out,
             int n_tokens, int vpr) {
   const int row = wave_row();
   if (row >= n_tokens) return;
   const long long id = ids[row];
-  copy_row<4>(table + id * vpr * 8, out + (size_t)row * vpr * 8, vpr, threadIdx.x & 63);
+  copy_row_kind<KIND>(table + id * vpr * 8, out + (size_t)row * vpr * 8, vpr, threadIdx.x & 63);
+}
+
+// Rows whose width is a multiple of 256 vectors (hidden % 2048 == 0), R rows per wave: for each
+// 256-vector slice, the R rows' loads (4 per lane per row) are all issued before any store, so
+// a wave keeps 16 * 4 * R bytes per lane in flight. Groups of R consecutive tokens are dealt to
+// the waves round-robin; the host sizes the grid at one 4-wave block per CU at most. The R ids
+// of a group arrive with one vector load (lane h reads id h) and are broadcast with readlane.
+template <int R>
+__global__ void __launch_bounds__(256)
+k_embedding_rows(const f16* __restrict__ table, const int* __restrict__ ids,
+                 f16* __restrict__ out, int n_tokens, int vpr) {
+  const int lane = threadIdx.x & 63;
+  const int n_groups = (n_tokens + R - 1) / R;
+  const int n_waves = gridDim.x * (blockDim.x >> 6);
+  for (int g = wave_row(); g < n_groups; g += n_waves) {
+    const int row0 = g * R;
+    const int my_id = lane < R && row0 + lane < n_tokens ? ids[row0 + lane] : 0;
+    long long off[R];  // offsets, not pointers: loads index the restrict-qualified table
+#pragma unroll
+    for (int h = 0; h < R; ++h)
+      off[h] = (long long)__builtin_amdgcn_readlane(my_id, h) * vpr * 8;
+    for (int v0 = 0; v0 < vpr; v0 += 256) {
+      u32x4 r[4 * R];
+#pragma unroll
+      for (int h = 0; h < R; ++h)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          r[4 * h + m] = ld16_stream(table + off[h] + 8 * (v0 + lane + 64 * m));
+      // Keep the scheduler from sinking loads below stores to save registers: the point is to
+      // have all 4 * R loads in flight at once.
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int h = 0; h < R; ++h) {
+        if (row0 + h < n_tokens) {
+          f16* dst = out + (size_t)(row0 + h) * vpr * 8;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) st16_stream(dst + 8 * (v0 + lane + 64 * m), r[4 * h + m]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
 }
 
 // BATCH: row b goes to position positions[b] of sequence b (table row b of `tables`).
 // otherwise: row t goes to position start_pos + t of the one sequence whose table is `tables`.
-template <bool BATCH>
+template <bool BATCH, int KIND>
 __global__ void __launch_bounds__(256)
 k_kv_scatter(const f16* __restrict__ src, f16* __restrict__ pool, const int* __restrict__ tables,
              const int* __restrict__ positions, int start_pos, int n_rows, int max_pages,
@@ -56,7 +113,7 @@ k_kv_scatter(const f16* __restrict__ src, f16* __restrict__ pool, const int* __r
   const int p = BATCH ? positions[row] : start_pos + row;
   const int* table = BATCH ? tables + (size_t)row * max_pages : tables;
   const long long prow = (long long)table[p / page_size] * page_size + p % page_size;
-  copy_row<4>(src + (size_t)row * vpr * 8, pool + prow * vpr * 8, vpr, threadIdx.x & 63);
+  copy_row_kind<KIND>(src + (size_t)row * vpr * 8, pool + prow * vpr * 8, vpr, threadIdx.x & 63);
 }
 
 template <int UNROLL>
@@ -94,11 +151,53 @@ extern "C" int llmk_embedding_lookup(const uint16_t* table, const int32_t* ids, 
   if (!table || !ids || !out) return LLMK_ERR_INVALID_VALUE;
   if (hidden % 8 != 0) return LLMK_ERR_SHAPE;
   if (!aligned16(table) || !aligned16(out)) return LLMK_ERR_ALIGNMENT;
+  const int vpr = hidden / 8;
+  if (vpr % 256 == 0 && n_tokens > 1024) {
+    // 1024 waves (4 per CU, one block per CU), each moving R rows at a time: at 8192 tokens of
+    // 2048 this measured 12.0 us against 13.9 us for one row per wave.
+    const int R = n_tokens >= 8 * 1024 ? 8 : (n_tokens >= 4 * 1024 ? 4 : 2);
+    const int groups = (n_tokens + R - 1) / R;
+    const unsigned blocks = ceil_div((size_t)(groups < 1024 ? groups : 1024), 4);
+    auto go = [&](auto kern) {
+      return launch(kern, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                    reinterpret_cast<const f16*>(table), ids, reinterpret_cast<f16*>(out),
+                    n_tokens, vpr);
+    };
+    if (R == 8) return go(k_embedding_rows<8>);
+    if (R == 4) return go(k_embedding_rows<4>);
+    return go(k_embedding_rows<2>);
+  }
   int wpb;
   const dim3 grid = rows_grid(n_tokens, &wpb);
-  return launch(k_embedding, grid, dim3(64 * wpb), 0, static_cast<hipStream_t>(stream),
-                reinterpret_cast<const f16*>(table), ids, reinterpret_cast<f16*>(out), n_tokens,
-                hidden / 8);
+  auto go = [&](auto kern) {
+    return launch(kern, grid, dim3(64 * wpb), 0, static_cast<hipStream_t>(stream),
+                  reinterpret_cast<const f16*>(table), ids, reinterpret_cast<f16*>(out), n_tokens,
+                  vpr);
+  };
+  switch (row_kind(vpr)) {
+    case 0: return go(k_embedding<0>);
+    case 1: return go(k_embedding<1>);
+    default: return go(k_embedding<2>);
+  }
+}
+
+template <bool BATCH>
+static int scatter_launch(const uint16_t* src, uint16_t* pool, const int32_t* tables,
+                          const int32_t* positions, int start_pos, int n_rows, int max_pages,
+                          int page_size, int kvdim, void* stream) {
+  int wpb;
+  const dim3 grid = rows_grid(n_rows, &wpb);
+  const int vpr = kvdim / 8;
+  auto go = [&](auto kern) {
+    return launch(kern, grid, dim3(64 * wpb), 0, static_cast<hipStream_t>(stream),
+                  reinterpret_cast<const f16*>(src), reinterpret_cast<f16*>(pool), tables,
+                  positions, start_pos, n_rows, max_pages, page_size, vpr);
+  };
+  switch (row_kind(vpr)) {
+    case 0: return go(k_kv_scatter<BATCH, 0>);
+    case 1: return go(k_kv_scatter<BATCH, 1>);
+    default: return go(k_kv_scatter<BATCH, 2>);
+  }
 }
 
 static int check_scatter(const void* src, const void* pool, const void* table, int n_rows,
@@ -116,11 +215,8 @@ extern "C" int llmk_kv_scatter(const uint16_t* src, uint16_t* pool, const int32_
   const int st = check_scatter(src, pool, block_table, T, page_size, kvdim);
   if (st != -1) return st;
   if (start_pos < 0) return LLMK_ERR_INVALID_VALUE;
-  int wpb;
-  const dim3 grid = rows_grid(T, &wpb);
-  return launch(k_kv_scatter<false>, grid, dim3(64 * wpb), 0, static_cast<hipStream_t>(stream),
-                reinterpret_cast<const f16*>(src), reinterpret_cast<f16*>(pool), block_table,
-                (const int*)nullptr, start_pos, T, 0, page_size, kvdim / 8);
+  return scatter_launch<false>(src, pool, block_table, nullptr, start_pos, T, 0, page_size, kvdim,
+                               stream);
 }
 
 extern "C" int llmk_kv_scatter_batch(const uint16_t* src, uint16_t* pool,
@@ -129,11 +225,8 @@ extern "C" int llmk_kv_scatter_batch(const uint16_t* src, uint16_t* pool,
   const int st = check_scatter(src, pool, block_tables, n, page_size, kvdim);
   if (st != -1) return st;
   if (!positions || max_pages <= 0) return LLMK_ERR_INVALID_VALUE;
-  int wpb;
-  const dim3 grid = rows_grid(n, &wpb);
-  return launch(k_kv_scatter<true>, grid, dim3(64 * wpb), 0, static_cast<hipStream_t>(stream),
-                reinterpret_cast<const f16*>(src), reinterpret_cast<f16*>(pool), block_tables,
-                positions, 0, n, max_pages, page_size, kvdim / 8);
+  return scatter_launch<true>(src, pool, block_tables, positions, 0, n, max_pages, page_size,
+                              kvdim, stream);
 }
 
 extern "C" int llmk_copy_bytes(const void* src, void* dst, size_t nbytes, void* stream) {

@@ -7,13 +7,12 @@
 // r16(x1*s)). Once c and s are fp16 values, every remaining step is an fp16 multiply or add of
 // two fp16 values rounded to fp16, which the packed fp16 instructions compute bit for bit.
 //
-// Work split: a block owns `tpb` consecutive tokens. Phase 1 computes the tpb * head_dim/2 (cos,
-// sin) pairs once each and keeps them in LDS as fp16 (the reference evaluates sincosf once per
-// head, 40x as often). Phase 2 walks the (token, head, j) tasks: a
-// task loads the 16-byte vector j of the first half of one head row and vector j of the second
-// half, which hold exactly the 8 pairs (8j .. 8j+7, +head_dim/2), rotates them with four packed
-// multiplies and two packed adds per 2 values, and stores both vectors. Q and K rows are read
-// and written once each.
+// Work split: a block owns `tpb` consecutive tokens. Their Q rows, K rows (and V rows in the
+// fused variant) are contiguous runs of 16-byte vectors, walked so that each wave instruction
+// covers 1 KiB of consecutive memory; the two halves of each pair group meet through a
+// cross-lane move. The tpb * head_dim/2 (cos, sin) pairs are computed once each and shared
+// through LDS as fp16 (the reference evaluates sincosf once per head, 40x as often). Q and K are
+// read and written exactly once.
 //
 // Fused decode variant (replaces ref: engine/batched.cu:55-58): the K task writes its rotated
 // vectors to the K pool row of its sequence instead of back to k, and V tasks copy the value
@@ -52,13 +51,47 @@ __device__ __forceinline__ void cos_sin_f16(float a, f16* c, f16* s) {
   *s = (f16)sf;
 }
 
-// HV = 16-byte vectors per half head row (head_dim = 16 * HV).
-template <int HV, bool FUSED>
+// The 16 bytes held by lane (lane ^ HV) of the same wave. HV < 16 stays inside a 16-lane DPP
+// row: lanes with bit HV clear read lane + HV (row_shl), the others lane - HV (row_shr).
+template <int HV>
+__device__ __forceinline__ u32x4 partner_vec(u32x4 x, bool upper) {
+  u32x4 p;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int v = (int)x[c];
+    int r;
+    if (HV == 1) {
+      r = __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if (HV == 2) {
+      r = __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if (HV == 4 || HV == 8) {
+      const int hi = __builtin_amdgcn_mov_dpp(v, 0x100 + HV, 0xF, 0xF, false);  // row_shl:HV
+      const int lo = __builtin_amdgcn_mov_dpp(v, 0x110 + HV, 0xF, 0xF, false);  // row_shr:HV
+      r = upper ? lo : hi;
+    } else {
+      r = __shfl_xor(v, HV);
+    }
+    p[c] = (uint32_t)r;
+  }
+  return p;
+}
+
+// HV = 16-byte vectors per half head row (head_dim = 16 * HV); TASKS = vectors per thread.
+//
+// Layout: a block owns tpb consecutive tokens. Their Q rows form one contiguous run of
+// tpb * nh * 2HV vectors, their K rows another of tpb * nkv * 2HV (and, fused, V a third).
+// Thread tid takes vectors v = tid + m * blockDim of the concatenated runs, so every wave load
+// and store instruction covers 1 KiB of consecutive memory. The two halves of a pair group sit
+// in lanes l and l ^ HV (vector j and j + HV of the same head row); each lane fetches its
+// partner's 16 bytes with a cross-lane move and writes its own half:
+//   first half:  x1' = x1*c - x2*s        second half: x2' = x2*c + x1*s
+// All loads are issued before the (cos, sin) phase so their latency overlaps it.
+template <int HV, int TASKS, bool FUSED>
 __global__ void __launch_bounds__(256)
-k_rope_vec(f16* q, f16* k, const f16* __restrict__ v, f16* k_pool, f16* v_pool,
+k_rope_vec(f16* q, const f16* k, const f16* __restrict__ v, f16* k_out, f16* v_pool,
            const int* __restrict__ tables, const int* __restrict__ pos,
            const float* __restrict__ inv_freq, int n_tokens, int nh, int nkv, int tpb,
-           int max_pages, int page_size, FastDiv per_token_div) {
+           int max_pages, int page_size, FastDiv qdiv, FastDiv kdiv) {
   constexpr int HD = 16 * HV, HALF = 8 * HV;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   long long* pool_row = reinterpret_cast<long long*>(smem);       // [tpb] (FUSED only)
@@ -66,7 +99,22 @@ k_rope_vec(f16* q, f16* k, const f16* __restrict__ v, f16* k_pool, f16* v_pool,
 
   const int t0 = blockIdx.x * tpb;
   const int ntok = min(tpb, n_tokens - t0);
+  const int qv = ntok * nh * 2 * HV, kv = ntok * nkv * 2 * HV;
+  const int total = qv + (FUSED ? 2 : 1) * kv;
+  const size_t kvdim = (size_t)nkv * HD;
+  f16* qb = q + (size_t)t0 * nh * HD;
+  const f16* kb = k + (size_t)t0 * kvdim;
+  const f16* vb = FUSED ? v + (size_t)t0 * kvdim : nullptr;
 
+  u32x4 x[TASKS];
+#pragma unroll
+  for (int m = 0; m < TASKS; ++m) {
+    const int e = threadIdx.x + m * blockDim.x;
+    if (e < qv) x[m] = ld16_stream(qb + 8 * e);
+    else if (e < qv + kv) x[m] = ld16_stream(kb + 8 * (e - qv));
+    else if (FUSED && e < total) x[m] = ld16_stream(vb + 8 * (e - qv - kv));
+    else x[m] = u32x4{0, 0, 0, 0};
+  }
   for (int e = threadIdx.x; e < ntok * HALF; e += blockDim.x) {
     const int tt = e / HALF, i = e % HALF;
     cos_sin_f16((float)pos[t0 + tt] * inv_freq[i], cs + tt * HD + i, cs + tt * HD + HALF + i);
@@ -80,41 +128,38 @@ k_rope_vec(f16* q, f16* k, const f16* __restrict__ v, f16* k_pool, f16* v_pool,
   }
   __syncthreads();
 
-  // Tasks per token: nh + nkv rotated heads, plus nkv value rows in the fused variant.
-  const int rows_per_tok = nh + nkv + (FUSED ? nkv : 0);
-  const int tasks = ntok * rows_per_tok * HV;
-  const size_t kvdim = (size_t)nkv * HD;
-  for (int e = threadIdx.x; e < tasks; e += blockDim.x) {
-    const int tt = (int)fdiv((uint32_t)e, per_token_div);
-    const int r = e - tt * rows_per_tok * HV;
-    const int head = r / HV, j = r % HV;
-    const int t = t0 + tt;
-    if (FUSED && head >= nh + nkv) {  // value row: plain copy into the V pool
-      const int hv = head - nh - nkv;
-      const f16* src = v + (size_t)t * kvdim + (size_t)hv * HD + 8 * j;
-      f16* dst = v_pool + pool_row[tt] * kvdim + (size_t)hv * HD + 8 * j;
-      const u32x4 lo = ld16(src), hi = ld16(src + HALF);
-      st16(dst, lo);
-      st16(dst + HALF, hi);
-      continue;
+  const bool upper = (threadIdx.x & HV) != 0;  // this lane holds the second half of its group
+#pragma unroll
+  for (int m = 0; m < TASKS; ++m) {
+    const int e = threadIdx.x + m * blockDim.x;
+    // Every lane takes part in the exchange, in uniform control flow; pair groups never straddle
+    // the Q / K / V boundaries (all multiples of 2HV), so a Q or K lane's partner is valid.
+    const u32x4 p = partner_vec<HV>(x[m], upper);
+    if (FUSED && e >= qv + kv) {  // value vector: copied unchanged into the V pool row
+      if (e < total) {
+        const int r = e - qv - kv;
+        const int tt = (int)fdiv((uint32_t)r, kdiv);
+        st16_stream(v_pool + pool_row[tt] * kvdim + 8 * (r - tt * (int)kdiv.d), x[m]);
+      }
+    } else if (e < qv + kv) {
+      int tt;
+      f16* dst;
+      if (e < qv) {
+        tt = (int)fdiv((uint32_t)e, qdiv);
+        dst = qb + 8 * e;
+      } else {
+        const int r = e - qv;
+        tt = (int)fdiv((uint32_t)r, kdiv);
+        dst = FUSED ? k_out + pool_row[tt] * kvdim + 8 * (r - tt * (int)kdiv.d)
+                    : k_out + (size_t)t0 * kvdim + 8 * r;
+      }
+      const int j = e & (HV - 1);
+      const f16x8 c = *reinterpret_cast<const f16x8*>(cs + tt * HD + 8 * j);
+      const f16x8 s = *reinterpret_cast<const f16x8*>(cs + tt * HD + HALF + 8 * j);
+      const f16x8 own = as_h8(x[m]), oth = as_h8(p);
+      const f16x8 y = upper ? own * c + oth * s : own * c - oth * s;
+      st16_stream(dst, as_u4(y));
     }
-    const f16* src;
-    f16* dst;
-    if (head < nh) {
-      src = dst = q + ((size_t)t * nh + head) * HD + 8 * j;
-    } else {
-      const int kh = head - nh;
-      src = k + (size_t)t * kvdim + (size_t)kh * HD + 8 * j;
-      dst = FUSED ? k_pool + pool_row[tt] * kvdim + (size_t)kh * HD + 8 * j
-                  : const_cast<f16*>(src);
-    }
-    const f16x8 x1 = as_h8(ld16(src)), x2 = as_h8(ld16(src + HALF));
-    const f16x8 c = *reinterpret_cast<const f16x8*>(cs + tt * HD + 8 * j);
-    const f16x8 s = *reinterpret_cast<const f16x8*>(cs + tt * HD + HALF + 8 * j);
-    const f16x8 y1 = x1 * c - x2 * s;
-    const f16x8 y2 = x2 * c + x1 * s;
-    st16(dst, as_u4(y1));
-    st16(dst + HALF, as_u4(y2));
   }
 }
 
@@ -146,41 +191,50 @@ k_rope_scalar(f16* q, f16* k, const int* __restrict__ pos, const float* __restri
   }
 }
 
-// Tokens per block: enough blocks to cover every CU, but at most 8 tokens (256 angles) per block.
+// Tokens per block: about 1024 blocks for long runs, one token per block for short ones.
 static int tokens_per_block(int n_tokens) {
-  if (n_tokens >= 8 * 2048) return 8;
-  if (n_tokens >= 4 * 1024) return 4;
-  if (n_tokens >= 2 * 512) return 2;
-  return 1;
+  int tpb = 1;
+  while (tpb < 16 && n_tokens / (2 * tpb) >= 1024) tpb *= 2;
+  return tpb;
 }
 
 template <bool FUSED>
-static int rope_vec_launch(f16* q, f16* k, const f16* v, f16* k_pool, f16* v_pool,
+static int rope_vec_launch(f16* q, const f16* k, const f16* v, f16* k_out, f16* v_pool,
                            const int* tables, const int* pos, const float* inv_freq,
                            int n_tokens, int nh, int nkv, int hd, int max_pages, int page_size,
                            hipStream_t stream) {
-  const int tpb = tokens_per_block(n_tokens);
   const int hv = hd / 16;
-  const int rows_per_tok = nh + nkv + (FUSED ? nkv : 0);
-  const FastDiv fd = make_fastdiv((uint32_t)(rows_per_tok * hv));
-  const int tasks_per_block = tpb * rows_per_tok * hv;
-  const int threads = tasks_per_block >= 1024 ? 256 : (tasks_per_block >= 256 ? 128 : 64);
-  const dim3 grid(ceil_div((size_t)n_tokens, (size_t)tpb)), block(threads);
+  const int per_tok = (nh + nkv + (FUSED ? nkv : 0)) * 2 * hv;  // vectors per token
+  constexpr int kThreads = 256, kMaxTasks = 16;
+  int tpb = tokens_per_block(n_tokens);
+  while (tpb > 1 && ceil_div((size_t)tpb * per_tok, kThreads) > (unsigned)kMaxTasks) tpb /= 2;
+  const unsigned tasks = ceil_div((size_t)tpb * per_tok, kThreads);
+  if (tasks > (unsigned)kMaxTasks) return LLMK_ERR_UNSUPPORTED;
+  const FastDiv qdiv = make_fastdiv((uint32_t)(nh > 0 ? nh * 2 * hv : 1));
+  const FastDiv kdiv = make_fastdiv((uint32_t)(nkv > 0 ? nkv * 2 * hv : 1));
+  const dim3 grid(ceil_div((size_t)n_tokens, (size_t)tpb)), block(kThreads);
   const size_t lds = (FUSED ? 8 * (size_t)tpb : 0) + (size_t)tpb * hd * sizeof(f16);
-#define LLMK_ROPE_CASE(H)                                                                       \
-  case H:                                                                                       \
-    return launch(k_rope_vec<H, FUSED>, grid, block, lds, stream, q, k, v, k_pool, v_pool,     \
-                  tables, pos, inv_freq, n_tokens, nh, nkv, tpb, max_pages, page_size, fd)
+#define LLMK_ROPE_LAUNCH(H, TK)                                                                  \
+  return launch(k_rope_vec<H, TK, FUSED>, grid, block, lds, stream, q, k, v, k_out, v_pool,     \
+                tables, pos, inv_freq, n_tokens, nh, nkv, tpb, max_pages, page_size, qdiv, kdiv)
+#define LLMK_ROPE_CASE(H)                \
+  case H:                                \
+    if (tasks <= 2) LLMK_ROPE_LAUNCH(H, 2);  \
+    if (tasks <= 4) LLMK_ROPE_LAUNCH(H, 4);  \
+    if (tasks <= 8) LLMK_ROPE_LAUNCH(H, 8);  \
+    if (tasks <= 12) LLMK_ROPE_LAUNCH(H, 12); \
+    LLMK_ROPE_LAUNCH(H, 16);
   switch (hv) {
-    LLMK_ROPE_CASE(1);
-    LLMK_ROPE_CASE(2);
-    LLMK_ROPE_CASE(4);
-    LLMK_ROPE_CASE(8);
-    LLMK_ROPE_CASE(16);
+    LLMK_ROPE_CASE(1)
+    LLMK_ROPE_CASE(2)
+    LLMK_ROPE_CASE(4)
+    LLMK_ROPE_CASE(8)
+    LLMK_ROPE_CASE(16)
     default:
       return LLMK_ERR_UNSUPPORTED;
   }
 #undef LLMK_ROPE_CASE
+#undef LLMK_ROPE_LAUNCH
 }
 
 }  // namespace llmk
@@ -204,9 +258,12 @@ extern "C" int llmk_rope_apply(uint16_t* q, uint16_t* k, const int32_t* position
   hipStream_t s = static_cast<hipStream_t>(stream);
   f16* pq = reinterpret_cast<f16*>(q);
   f16* pk = reinterpret_cast<f16*>(k);
-  if (vec_head_dim(head_dim) && aligned16(q) && aligned16(k))
-    return rope_vec_launch<false>(pq, pk, nullptr, nullptr, nullptr, nullptr, positions,
-                                  inv_freq, n_tokens, n_heads, n_kv_heads, head_dim, 0, 1, s);
+  if (vec_head_dim(head_dim) && aligned16(q) && aligned16(k)) {
+    const int st = rope_vec_launch<false>(pq, pk, nullptr, pk, nullptr, nullptr, positions,
+                                          inv_freq, n_tokens, n_heads, n_kv_heads, head_dim, 0,
+                                          1, s);
+    if (st != LLMK_ERR_UNSUPPORTED) return st;  // else: a token too wide for one block
+  }
   if (head_dim > 4096) return LLMK_ERR_UNSUPPORTED;
   const int tpb = tokens_per_block(n_tokens);
   return launch(k_rope_scalar, dim3(ceil_div((size_t)n_tokens, (size_t)tpb)), dim3(256),
@@ -232,7 +289,7 @@ extern "C" int llmk_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const 
       !aligned16(v_pool))
     return LLMK_ERR_ALIGNMENT;
   return rope_vec_launch<true>(
-      reinterpret_cast<f16*>(q), const_cast<f16*>(reinterpret_cast<const f16*>(k)),
+      reinterpret_cast<f16*>(q), reinterpret_cast<const f16*>(k),
       reinterpret_cast<const f16*>(v), reinterpret_cast<f16*>(k_pool),
       reinterpret_cast<f16*>(v_pool), block_tables, positions, inv_freq, n, n_heads, n_kv_heads,
       head_dim, max_pages, page_size, static_cast<hipStream_t>(stream));

@@ -166,6 +166,10 @@ ROPE_SHAPES = [  # (T, n_heads, n_kv_heads, head_dim)
     (17, 16, 4, 128), (9, 8, 2, 256), (33, 4, 1, 32), (6, 3, 1, 16),
     (7, 32, 0, 64), (5, 0, 8, 64),
     (11, 4, 2, 40), (3, 2, 1, 6),  # head_dim not a multiple of 16: scalar path
+    (16385, 32, 8, 64),            # 8 tokens per block
+    (33001, 4, 1, 64),             # 16 tokens per block, partial last block
+    (7, 64, 8, 256),               # wide tokens: 12 vectors per thread
+    (2, 128, 32, 256),             # one token exceeds a block: scalar path
 ]
 
 
@@ -217,6 +221,27 @@ def test_swiglu(llmk, orc, n, offset):
     got = host(bo)
     assert_tol(orc.compare(got[offset:offset + n], orc.swiglu(g, u)), 0.995, "swiglu")
     assert np.all(got[offset + n:] == CANARY)
+
+
+@pytest.mark.parametrize("up_value", [1.0, -1.5, 0.0999, 7.0, 65504.0])
+def test_swiglu_all_fp16_gate_values_bit_exact(llmk, orc, up_value):
+    """silu depends on the 16-bit gate only: every one of the 65536 fp16 gate values (NaNs,
+    infinities, subnormals included) gives the oracle's bits, in the vector kernel and in the
+    any-alignment kernel."""
+    gate = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    up = np.full(65536, up_value, np.float16).view(np.uint16)
+    with np.errstate(all="ignore"):
+        exp = orc.swiglu(gate, up)
+    for offset in (0, 1):
+        bg, bu, bo = filled(65536 + offset), filled(65536 + offset), filled(65536 + offset)
+        bg[offset:] = dev(gate)
+        bu[offset:] = dev(up)
+        llmk.swiglu(bg[offset:], bu[offset:], bo[offset:], 65536)
+        got = host(bo)[offset:]
+        nan = np.isnan(exp.view(np.float16))
+        assert np.array_equal(np.isnan(got.view(np.float16)), nan)
+        bad = np.flatnonzero((got != exp) & ~nan)
+        assert bad.size == 0, f"offset {offset}: gate values {gate[bad[:8]]} differ"
 
 
 def test_swiglu_special_values(llmk, orc):
@@ -300,6 +325,17 @@ def test_rope_kv_scatter_batch(llmk, orc, n, nh, nkv, hd):
     assert np.array_equal(host(dk), k), "k is read only"
     if nh:
         assert_tol(orc.compare(host(dq), q_e), 0.995, "Q")
+
+
+def test_rope_kv_scatter_batch_rejects_a_token_wider_than_a_block(llmk, orc):
+    n, nh, nkv, hd = 2, 128, 32, 256
+    _, dinv = inv_freq_dev(orc, hd)
+    q, k = filled(n * nh * hd), filled(n * nkv * hd)
+    pool = filled(16 * nkv * hd)
+    tab, pos = dev_i32(np.zeros((n, 1), np.int32)), dev_i32(np.zeros(n, np.int32))
+    with pytest.raises(llmk.LlmkError, match="outside what the kernels implement"):
+        llmk.rope_kv_scatter_batch(q, k, k, pool, pool, tab, pos, dinv, n, 1, 16, nh, nkv, hd)
+    assert np.all(host(pool) == POISON)
 
 
 def test_rope_kv_scatter_batch_equals_the_three_reference_launches(llmk, orc):
