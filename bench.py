@@ -36,7 +36,7 @@ METRIC = ("achieved HBM GB/s (% of ~8 TB/s) per fused kernel; "
           "µs per 16-layer non-GEMM pass")
 PEAK_GBS = 8000.0
 WARM_S = 0.25
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "nongemm_kernels_counters_traffic.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "llmk_kernels_bench_configs.txt")
 
 
 def log(msg: str) -> None:
@@ -117,12 +117,29 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
                 if name in r["Kernel_Name"] and grid(r) == g:
                     cnt.setdefault((label, cname), []).append(float(r["Counter_Value"]))
     avg = {k: sum(v) / len(v) for k, v in cnt.items() if v}
+    print("# rocprofv3 summaries of bench.py on one MI355X (gfx950), made by:")
+    print(f"#   rocprofv3 --kernel-trace --stats -f csv -d {trace_dir} -o bench -- "
+          "python3 bench.py --no-cpu")
+    print(f"#   rocprofv3 --pmc FETCH_SIZE -f csv -d {fetch_dir} -o fetch -- "
+          "python3 bench.py --no-cpu --steps 20 --warmup 2")
+    print(f"#   rocprofv3 --pmc WRITE_SIZE -f csv -d {write_dir} -o write -- "
+          "python3 bench.py --no-cpu --steps 20 --warmup 2")
+    print(f"#   python3 bench.py --summarize-profiles {trace_dir} {fetch_dir} {write_dir}")
+    print("#")
+    print("# rocprofv3 --stats, libllmk kernels (all launch shapes of the run together):")
+    print("#   calls  avg_us  min_us  max_us  kernel")
+    for r in rows(trace_dir, "kernel_stats.csv"):
+        if "llmk" in r["Name"]:
+            print(f"#   {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:8.3f} "
+                  f"{float(r['MinNs']) / 1e3:8.3f} {float(r['MaxNs']) / 1e3:8.3f}  {r['Name'][:90]}")
+    print("#")
     copy_b = 1 << 30
     sf = copy_b / (avg[("copy_1GiB", "FETCH_SIZE")] * 1024)
     sw = copy_b / (avg[("copy_1GiB", "WRITE_SIZE")] * 1024)
-    print(f"# FETCH_SIZE scale {sf:.4f}, WRITE_SIZE scale {sw:.4f} "
-          f"(copy probe: 1 GiB read and 1 GiB written per launch)")
-    print("# label  us_mean  calls  fetch_kib  write_kib  traffic_bytes  algorithmic_bytes  ratio")
+    print(f"# Per launch shape. us_mean: mean kernel duration in the kernel trace. fetch_kib and")
+    print(f"# write_kib: FETCH_SIZE and WRITE_SIZE per dispatch. traffic_bytes = fetch_kib*1024*"
+          f"{sf:.4f} + write_kib*1024*{sw:.4f}, the factors being 1 GiB over what each counter")
+    print("# reads for the 1 GiB copy probe (1 GiB read and 1 GiB written per launch).")
     for label, _, _, alg in PROFILE_SHAPES:
         d = dur.get(label, [])
         f, w = avg.get((label, "FETCH_SIZE")), avg.get((label, "WRITE_SIZE"))
@@ -139,11 +156,11 @@ class Timer:
     """Two timed passes of `steps` launches each.
 
     1. Host wall clock: `steps` back-to-back launches, torch.cuda.synchronize() on both sides.
-    2. HIP events: the stream is first held by a short spin kernel while filler launches (3 ms
-       of GPU time, to bring clocks back up) and then the `steps` timed launches are enqueued
-       behind it, with one event recorded right before the first timed launch and one right
-       after the last, on the launching stream. The mean launch duration is the event interval
-       / steps: the GPU runs the launches back to back, so host-side enqueue time is excluded.
+    2. HIP events: filler launches (3 ms of GPU time) and then the `steps` timed launches are
+       enqueued back to back, with one event recorded right before the first timed launch and one
+       right after the last, on the launching stream. Where the host enqueues more slowly than
+       the GPU executes, a spin kernel holds the stream until all of it is enqueued. The mean
+       launch duration is the event interval / steps: the launches run back to back on the GPU.
     """
 
     def __init__(self, torch):
@@ -184,14 +201,17 @@ class Timer:
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
 
-        # Event pass. The stream is held by a spin kernel while everything is enqueued; behind
-        # it, `fill` launches of the same kernel (at least 3 ms of GPU time) bring the clocks
-        # back up from the spin kernel's idle load before the start event.
+        # Event pass: `fill` launches of the same kernel (at least 3 ms of GPU time) run ahead of
+        # the start event, so the queue is full and the clocks are up when timing starts. When
+        # the host enqueues more slowly than the GPU executes (short kernels), the stream is
+        # first held by a spin kernel until everything is enqueued.
         stream = torch.cuda.current_stream()
         fill = min(4000, max(8, int(3e-3 / max(wall / steps, 1e-7))))
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        hold = max(2e-3, 3 * enq * (fill + steps))
-        torch.cuda._sleep(int(hold * self.cycles_per_s))
+        host_bound = enq > 0.5 * wall / steps
+        hold = 3 * enq * (fill + steps) if host_bound else 0.0
+        if host_bound:
+            torch.cuda._sleep(int(hold * self.cycles_per_s))
         t1 = time.perf_counter()
         for i in range(fill):
             launch(i % n_sets)
@@ -203,7 +223,8 @@ class Timer:
         torch.cuda.synchronize()
         ev = a.elapsed_time(b) * 1e-3
         return {"wall_s": wall, "mean_s": ev / steps, "event_s": ev, "enqueue_s": enqueue,
-                "hold_s": hold, "queue_prefilled": enqueue < hold, "steps": steps}
+                "hold_s": hold, "host_bound": host_bound,
+                "queue_prefilled": (enqueue < hold) if host_bound else True, "steps": steps}
 
 
 def kernel_entry(name, nbytes, t, traffic=None, extra=None):
