@@ -73,6 +73,11 @@ def read_traffic() -> dict:
 
 # (label, kernel-name substring, grid size in work-items, algorithmic bytes) of each measured
 # launch shape; grid sizes follow from the launchers' grid choices at the benchmark shapes.
+# Decode attention over 256 sequences with lengths uniform in [1, 2048] (seed 0x5EED0006):
+# the bytes of bytes_attention(attention_lens()) in cuda-llm-engine_amd/workloads.py.
+ATTN_BYTES_256 = 546_019_628
+ATTN_BYTES_16x2048 = 67_248_192  # 16 sequences x 2048 positions
+
 PROFILE_SHAPES = [
     ("add_rmsnorm_8192x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 8192 * 64, 134221824),
     ("rmsnorm_16x2048", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
@@ -80,6 +85,10 @@ PROFILE_SHAPES = [
     ("swiglu_8192x8192", "k_swiglu_vecILi2E", 16384 * 256, 402653184),
     ("embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
     ("copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),
+    ("attention_decode_256", "k_attn_balancedILi8E", 1024 * 256, ATTN_BYTES_256,
+     ("k_attn_merge", 256 * 256)),
+    ("attention_decode_16x2048", "k_attn_balancedILi8E", 1024 * 256, ATTN_BYTES_16x2048,
+     ("k_attn_merge", 256 * 16)),
     ("decode:embedding_256", "k_embeddingILi0E", 256 * 64, 2098176),
     ("decode:add_rmsnorm_256x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 256 * 64, 4198400),
     ("decode:rope_kv_scatter_256", "k_rope_vecILi4ELi2ELb1E", 256 * 256, 3147904),
@@ -101,21 +110,35 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
         return out
 
     def grid(r):
-        return int(r.get("Grid_Size_X") or r.get("Grid_Size"))
+        if "Grid_Size_X" in r:
+            return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        return int(r["Grid_Size"])
+
+    def matches(table):
+        """(label, row) for every row of a launch shape; a shape with a 5th field also needs
+        the next dispatch to be that (kernel, grid) -- the attention kernel is told apart by
+        the merge launch that follows it."""
+        by_id = {int(r["Dispatch_Id"]): r for r in table}
+        for r in table:
+            for shape in PROFILE_SHAPES:
+                label, name, g = shape[:3]
+                if name not in r["Kernel_Name"] or grid(r) != g:
+                    continue
+                if len(shape) > 4:
+                    nxt = by_id.get(int(r["Dispatch_Id"]) + 1)
+                    if nxt is None or shape[4][0] not in nxt["Kernel_Name"] \
+                            or grid(nxt) != shape[4][1]:
+                        continue
+                yield label, r
 
     dur, cnt = {}, {}
-    for r in rows(trace_dir, "kernel_trace.csv"):
-        for label, name, g, _ in PROFILE_SHAPES:
-            if name in r["Kernel_Name"] and grid(r) == g:
-                dur.setdefault(label, []).append(
-                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+    for label, r in matches(rows(trace_dir, "kernel_trace.csv")):
+        dur.setdefault(label, []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
     for d, cname in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
-        for r in rows(d, "counter_collection.csv"):
-            if r["Counter_Name"] != cname:
-                continue
-            for label, name, g, _ in PROFILE_SHAPES:
-                if name in r["Kernel_Name"] and grid(r) == g:
-                    cnt.setdefault((label, cname), []).append(float(r["Counter_Value"]))
+        table = [r for r in rows(d, "counter_collection.csv") if r["Counter_Name"] == cname]
+        for label, r in matches(table):
+            cnt.setdefault((label, cname), []).append(float(r["Counter_Value"]))
     avg = {k: sum(v) / len(v) for k, v in cnt.items() if v}
     print("# rocprofv3 summaries of bench.py on one MI355X (gfx950), made by:")
     print(f"#   rocprofv3 --kernel-trace --stats -f csv -d {trace_dir} -o bench -- "
@@ -140,7 +163,7 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
     print(f"# write_kib: FETCH_SIZE and WRITE_SIZE per dispatch. traffic_bytes = fetch_kib*1024*"
           f"{sf:.4f} + write_kib*1024*{sw:.4f}, the factors being 1 GiB over what each counter")
     print("# reads for the 1 GiB copy probe (1 GiB read and 1 GiB written per launch).")
-    for label, _, _, alg in PROFILE_SHAPES:
+    for label, _, _, alg, *_ in PROFILE_SHAPES:
         d = dur.get(label, [])
         f, w = avg.get((label, "FETCH_SIZE")), avg.get((label, "WRITE_SIZE"))
         us = f"{sum(d) / len(d):.3f}" if d else "-"
@@ -255,7 +278,7 @@ def main() -> int:
         print(f"bench.py measures one GPU only (the kernels are single-GPU; this build has no "
               f"multi-GPU path): --gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
-    import numpy as np  # noqa: F401
+    import numpy as np
     import torch
 
     sys.path.insert(0, ROOT)
@@ -371,6 +394,35 @@ def main() -> int:
             "decode pass 16 layers x 256 (eager)", wl.bytes_decode_pass(256, 16), t)
         del p, dp, graph, table
         torch.cuda.empty_cache()
+
+        # decode attention over the paged pool (the pool's consumer): 256 sequences with
+        # lengths uniform in [1, 2048], and the reference's bench shape, 16 sequences x 2048
+        # (ref: bench/bench_attention_compare.cu). Split count: choose_num_splits' default.
+        lens = wl.attention_lens()
+        nb_attn = wl.bytes_attention(lens)
+        if nb_attn != ATTN_BYTES_256:
+            raise RuntimeError(f"attention workload bytes {nb_attn} != {ATTN_BYTES_256}")
+        for label, lens_b, R6 in (("attention_decode_256", lens, 2),
+                                  ("attention_decode_16x2048", np.full(16, 2048), 17)):
+            splits = llmk.choose_num_splits(lens_b.size, wl.N_KV, int(lens_b.max()))
+            sets6 = [wl.attention_inputs(lens_b, num_splits=splits,
+                                         seed=wl.SEED_BASE + 6 + 100 * i) for i in range(R6)]
+
+            def launch_attn(i, sets6=sets6, splits=splits):
+                a = sets6[i]
+                llmk.attention_decode_fast(a["q"], a["k_pool"], a["v_pool"], a["block_tables"],
+                                           a["seq_lens"], a["out"], a["workspace"], a["n"],
+                                           a["max_pages"], wl.PAGE, wl.N_HEADS, wl.N_KV,
+                                           wl.HEAD_DIM, splits, check_indices=False)
+
+            t = timer.run(launch_attn, R6, K, W)
+            kernels[label] = kernel_entry(
+                f"attention_decode_fast {label.split('_')[-1]}", wl.bytes_attention(lens_b), t,
+                traffic.get(label), {"sets": R6, "num_splits": splits, "seqs": int(lens_b.size),
+                                     "context_tokens": int(lens_b.sum()),
+                                     "launches": 2, "note": "page-balanced split + merge"})
+            del sets6
+            torch.cuda.empty_cache()
 
         # copy probe: practical HBM ceiling (ref: bench/bandwidth.cu)
         nb = 1 << 30

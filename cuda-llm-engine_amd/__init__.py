@@ -81,6 +81,8 @@ _SIGS = {
     "llmk_kv_scatter_batch": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "llmk_rope_kv_scatter_batch": (_i, [_vp] * 8 + [_i] * 6 + [_vp]),
     "llmk_copy_bytes": (_i, [_vp, _vp, _sz, _vp]),
+    "llmk_attention_decode_fast_workspace_floats": (_sz, [_i, _i, _i]),
+    "llmk_attention_decode_fast": (_i, [_vp] * 7 + [_i] * 7 + [_vp]),
     "llmk_decode_nongemm_pass": (_i, [ctypes.POINTER(DecodePass), _vp]),
 }
 
@@ -295,6 +297,60 @@ def rope_kv_scatter_batch(q, k, v, k_pool, v_pool, block_tables, positions, inv_
     _check(fn, _lib.llmk_rope_kv_scatter_batch(pq, pk, pv, pkp, pvp, pt, pp, pf, n, max_pages,
                                                page_size, n_heads, n_kv_heads, head_dim,
                                                _stream(stream)))
+
+
+# Default of choose_num_splits; the same value as LLMK_ATTN_TARGET_BLOCKS in include/llmk.h.
+ATTN_TARGET_BLOCKS = 65536
+
+
+def choose_num_splits(n_seq: int, n_kv_heads: int, max_seq_len: int,
+                      target_blocks: int = ATTN_TARGET_BLOCKS) -> int:
+    """Split count for attention_decode_fast (ref: kernels/attention_decode_fast.cuh:22-29)."""
+    splits = target_blocks // (n_seq * n_kv_heads)
+    splits = min(splits, (max_seq_len + 15) // 16, 32)
+    return max(splits, 1)
+
+
+def attention_decode_fast_workspace_floats(n_seq: int, n_heads: int, num_splits: int) -> int:
+    """ref: kernels/attention_decode_fast.cuh:6"""
+    return int(_lib.llmk_attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits))
+
+
+def attention_decode_fast(q, k_pool, v_pool, block_tables, seq_lens, out, workspace, n_seq: int,
+                          max_pages: int, page_size: int, n_heads: int, n_kv_heads: int,
+                          head_dim: int, num_splits: int, stream=None,
+                          check_indices: bool = True) -> None:
+    """Split-KV decode attention over the paged pool (ref: kernels/attention_decode_fast.cuh:14-18).
+
+    With ``check_indices`` the binding also checks, on the host, that every sequence length
+    fits the block table (seq_lens <= max_pages * page_size) and that every page number a
+    cached position reads lies inside both pools."""
+    fn = "attention_decode_fast"
+    kvdim = n_kv_heads * head_dim
+    pq = _dev(fn, q, torch.float16, n_seq * n_heads * head_dim, "q")
+    pk = _dev(fn, k_pool, torch.float16, 0, "k_pool")
+    pv = _dev(fn, v_pool, torch.float16, 0, "v_pool")
+    pt = _dev(fn, block_tables, torch.int32, n_seq * max_pages, "block_tables")
+    pl = _dev(fn, seq_lens, torch.int32, n_seq, "seq_lens")
+    po = _dev(fn, out, torch.float16, n_seq * n_heads * head_dim, "out")
+    ws_need = attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits)
+    pw = 0
+    if workspace is not None:
+        pw = _dev(fn, workspace, torch.float32, ws_need if num_splits > 1 else 0, "workspace")
+    if check_indices and n_seq > 0 and max_pages > 0 and page_size > 0 and kvdim > 0:
+        _range_check(fn, seq_lens, n_seq, -(1 << 31), max_pages * page_size + 1, "seq_lens")
+        lens = seq_lens[:n_seq].long().clamp(min=0)
+        npages = (lens + page_size - 1) // page_size
+        tables = block_tables.reshape(-1)[:n_seq * max_pages].view(n_seq, max_pages)
+        used = torch.arange(max_pages, device=tables.device)[None, :] < npages[:, None]
+        if bool(used.any()):
+            rows = min(_pool_rows(fn, k_pool, kvdim), _pool_rows(fn, v_pool, kvdim))
+            pages = tables[used]
+            _range_check(fn, pages, pages.numel(), 0, rows // page_size,
+                         "block_tables (entries of cached positions)")
+    _check(fn, _lib.llmk_attention_decode_fast(pq, pk, pv, pt, pl, po, pw, n_seq, max_pages,
+                                               page_size, n_heads, n_kv_heads, head_dim,
+                                               num_splits, _stream(stream)))
 
 
 def copy_bytes(src, dst, nbytes: int, stream=None) -> None:

@@ -1,0 +1,663 @@
+// Decode attention over the paged KV pool, split over the cached positions (split-KV): one query
+// token per sequence against all of its cached K and V rows.
+//
+// Interface and workspace contract: ref kernels/attention_decode_fast.cuh:5-18 and
+// kernels/attention_decode_fast.cu:151-172 (page_size 16, head_dim 64, 4 query heads per kv
+// head; the caller's workspace of n_seq * n_heads * num_splits * 66 floats).
+// Values: those of the plain paged kernel the reference checks it against
+// (kernels/attention_decode_paged.cu:24-62): softmax over positions of q.k / sqrt(64), then the
+// weighted sum of the V rows, all in fp32, the result rounded once to fp16. Sums run in a
+// different order here, so results agree within the reference test's tolerance
+// (tests/test_attention_decode_fast.cu:83-91), not bit for bit.
+//
+// Layout on gfx950. A pool row holds one position's K (or V) for all n_kv heads: n_kv * 128
+// bytes, [kv head][64 dims]. A wave reads 1 KiB of it per instruction, 16 bytes per lane: lane
+// (octet o = lane / 8, d8 = lane % 8) holds dims 8*d8 .. 8*d8+7 of kv head o of one position
+// (for n_kv = 8; with 4, 2 or 1 kv heads per row the octets cover 2, 4 or 8 consecutive
+// positions, still one contiguous 1 KiB). The 8 lanes of an octet hold one (position, kv head):
+// their q.k partial dots meet in three DPP steps, and every lane then owns the scores of the 4
+// query heads that share its kv head.
+//
+// Each block (4 waves) takes one split: a run of up to `pages_per_split` pages of one sequence
+// for up to 8 kv heads. Waves take chunks of kChunk row reads in turn and keep an online softmax
+// per query head (running max m and sum l in log2 units, fp32 accumulators for their 8 dims),
+// rescaling once per chunk. The block merges its waves through LDS. A sequence that fits in one
+// split gets its output written directly; otherwise each split leaves an unnormalised partial
+// (A, m, l) in the workspace and a second kernel merges the splits.
+#include <math.h>
+
+#include "common.hpp"
+
+namespace llmk {
+namespace {
+
+constexpr int kHeadDim = 64;
+constexpr int kGroup = 4;  // query heads per kv head
+constexpr int kPage = 16;  // positions per page
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kChunk = 4;  // row reads per wave between softmax rescales
+// 1/sqrt(64) times log2(e): scores are kept in log2 units so that exp(x - m) is one v_exp_f32.
+constexpr float kScoreScale = 0.125f * 1.44269504088896341f;
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Element k of a 4 x 32-bit vector as a scalar. (The element is copied out before any
+// __builtin_bit_cast: this compiler lowers a bit_cast applied directly to a vector-element
+// expression as a read of element 0.)
+__device__ __forceinline__ uint32_t elem(u32x4 v, int k) {
+  const uint32_t e = v[k];
+  return e;
+}
+
+// Partial dot product of 8 fp16 dims (4 packed pairs), fp32 accumulation.
+__device__ __forceinline__ float dot8(u32x4 a, u32x4 b) {
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t ak = elem(a, k), bk = elem(b, k);
+    s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ak), __builtin_bit_cast(h2, bk), s, false);
+  }
+  return s;
+}
+
+// Sum over the 8 lanes of each octet; every lane of the octet gets the total.
+__device__ __forceinline__ float octet_sum(float x) {
+  x = x + dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
+  x = x + dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
+  x = x + dpp_f32<0x141>(x);  // row_half_mirror: lane i <-> 7 - i within each 8 lanes
+  return x;
+}
+
+// Pages of the sequence that hold cached positions, capped at the block table's width.
+__device__ __forceinline__ int seq_pages(int S, int max_pages) {
+  const int P = S > 0 ? (S + kPage - 1) / kPage : 0;
+  return P < max_pages ? P : max_pages;
+}
+
+struct SoftmaxState {
+  float m[kGroup], l[kGroup], acc[kGroup][8];
+};
+
+// Row reads per chunk: kChunk, fewer when a row read spans many positions, so that a chunk
+// never crosses a page (chunks start at multiples of their size within page-aligned ranges).
+template <int KVW>
+constexpr int chunk_rows() {
+  return kChunk * (8 / KVW) <= kPage ? kChunk : kPage / (8 / KVW);
+}
+
+// One chunk of row reads: rows [row0, row0 + ROWS) of this block's position range, all in one
+// page. FULL: every position in the chunk is cached (no per-lane tests).
+template <int KVW, bool FULL>
+__device__ __forceinline__ void attend_chunk(SoftmaxState& st, const u32x4 (&qv)[kGroup],
+                                             const f16* __restrict__ k_pool,
+                                             const f16* __restrict__ v_pool,
+                                             const int* __restrict__ table, int pos0, int pos1,
+                                             int row0, size_t row_halves, size_t lane_off,
+                                             int slot) {
+  constexpr int PPL = 8 / KVW;  // positions per row read
+  constexpr int ROWS = chunk_rows<KVW>();
+  const int cpos = pos0 + row0 * PPL;  // first position of the chunk (wave-uniform)
+  const int page = table[cpos / kPage];
+  const size_t base = ((size_t)page * kPage + (size_t)(cpos % kPage)) * row_halves + lane_off;
+  u32x4 kr[ROWS], vr[ROWS];
+  bool ok[ROWS];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const size_t off = base + (size_t)(r * PPL) * row_halves;
+    ok[r] = FULL || cpos + r * PPL + slot < pos1;
+    if (FULL) {
+      kr[r] = ld16_stream(k_pool + off);
+      vr[r] = ld16_stream(v_pool + off);
+    } else {
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      kr[r] = zero;
+      vr[r] = zero;
+      if (ok[r]) {
+        kr[r] = ld16_stream(k_pool + off);
+        vr[r] = ld16_stream(v_pool + off);
+      }
+    }
+  }
+  // Raw scores q.k (uncached positions: -inf); the scale is applied inside the exponent.
+  float s[ROWS][kGroup];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      const float d = octet_sum(dot8(qv[i], kr[r]));
+      s[r][i] = ok[r] ? d : -INFINITY;
+    }
+  float corr[kGroup], p[ROWS][kGroup];
+  bool grew = false;
+#pragma unroll
+  for (int i = 0; i < kGroup; ++i) {
+    float mx = s[0][i];
+#pragma unroll
+    for (int r = 1; r < ROWS; ++r) mx = fmaxf(mx, s[r][i]);
+    const float mn = fmaxf(st.m[i], mx * kScoreScale);
+    const float base = mn == -INFINITY ? 0.0f : mn;  // nothing seen yet: keep everything at 0
+    corr[i] = __builtin_amdgcn_exp2f(st.m[i] - base);
+    grew = grew || mn != st.m[i];
+    float psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      p[r][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r][i], kScoreScale, -base));
+      psum = psum + p[r][i];
+    }
+    st.l[i] = __builtin_fmaf(st.l[i], corr[i], psum);
+    st.m[i] = mn;
+  }
+  // The running max rarely grows once a few chunks are in; when it did not grow anywhere in the
+  // wave every correction factor is exactly 2^0 = 1 and the rescale is skipped.
+  if (__builtin_amdgcn_ballot_w64(grew)) {
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) st.acc[i][d] = st.acc[i][d] * corr[i];
+  }
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const f16x8 vh = as_h8(vr[r]);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const float v = (float)vh[d];
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i) st.acc[i][d] = __builtin_fmaf(p[r][i], v, st.acc[i][d]);
+    }
+  }
+}
+
+// Per-block LDS: the waves' softmax states for the merge at the end of a segment.
+template <int KVW>
+struct MergeLds {
+  static constexpr int NP = kWaves * (8 / KVW);  // partial states per query head
+  static constexpr int HEADS = KVW * kGroup;     // query heads a block serves (32 for KVW = 8)
+  float acc[NP][HEADS][kHeadDim];
+  float m[NP][HEADS], l[NP][HEADS];
+};
+
+// The block's attention over positions [pos0, pos1) of sequence `seq` (all cached, in the pages
+// of `table`) for the query heads of kv group `kvg`. On return thread t with t / 8 < HEADS holds
+// the block's combined unnormalised state of query head kvg * HEADS + t / 8, dims 8 * (t % 8)
+// .. + 8: A (sum of p * v), M (max score, log2 units) and L (sum of p). Ends with a barrier, so
+// the LDS can be reused at once.
+template <int KVW>
+__device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
+                                               const f16* __restrict__ k_pool,
+                                               const f16* __restrict__ v_pool,
+                                               const int* __restrict__ table, int seq, int pos0,
+                                               int pos1, int kvg, int n_heads, int n_kv_heads,
+                                               MergeLds<KVW>& lds, float (&A)[8], float& M,
+                                               float& L) {
+  constexpr int PPL = 8 / KVW;
+  constexpr int NP = MergeLds<KVW>::NP, HEADS = MergeLds<KVW>::HEADS;
+  constexpr int ROWS = chunk_rows<KVW>();
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int octet = lane >> 3, d8 = lane & 7;
+  const int slot = octet / KVW, kvl = octet % KVW;
+  const int kvh = kvg * 8 + kvl;
+  const size_t row_halves = (size_t)n_kv_heads * kHeadDim;
+  // Lane's offset inside a row read: this kv group's 8 heads, then 16 bytes per lane (for
+  // KVW < 8 the lanes run on into the next PPL - 1 rows, which are contiguous within a page).
+  const size_t lane_off = (size_t)kvg * 8 * kHeadDim + (size_t)lane * 8;
+
+  u32x4 qv[kGroup];
+#pragma unroll
+  for (int i = 0; i < kGroup; ++i)
+    qv[i] = ld16(q + ((size_t)seq * n_heads + kvh * kGroup + i) * kHeadDim + d8 * 8);
+
+  SoftmaxState st;
+#pragma unroll
+  for (int i = 0; i < kGroup; ++i) {
+    st.m[i] = -INFINITY;
+    st.l[i] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st.acc[i][d] = 0.0f;
+  }
+
+  const int n_rows = (pos1 - pos0 + PPL - 1) / PPL;
+  const int full_rows = (pos1 - pos0) / PPL;  // rows whose every position is cached
+  int row0 = wave * ROWS;
+  for (; row0 + ROWS <= full_rows; row0 += kWaves * ROWS)
+    attend_chunk<KVW, true>(st, qv, k_pool, v_pool, table, pos0, pos1, row0, row_halves,
+                            lane_off, slot);
+  if (row0 < n_rows)  // at most one partly cached chunk per wave
+    attend_chunk<KVW, false>(st, qv, k_pool, v_pool, table, pos0, pos1, row0, row_halves,
+                             lane_off, slot);
+
+  // Merge the NP partial states of every query head through LDS.
+  const int pi = wave * PPL + slot;
+#pragma unroll
+  for (int i = 0; i < kGroup; ++i) {
+    float* dst = &lds.acc[pi][kvl * kGroup + i][d8 * 8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) dst[d] = st.acc[i][d];
+    if (d8 == 0) {
+      lds.m[pi][kvl * kGroup + i] = st.m[i];
+      lds.l[pi][kvl * kGroup + i] = st.l[i];
+    }
+  }
+  __syncthreads();
+  const int hl = tid >> 3, e8 = tid & 7;
+  M = -INFINITY;
+  L = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) A[d] = 0.0f;
+  if (hl < HEADS) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) M = fmaxf(M, lds.m[k][hl]);
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const float w = __builtin_amdgcn_exp2f(lds.m[k][hl] - M);  // a state that saw nothing: 0
+      L = __builtin_fmaf(lds.l[k][hl], w, L);
+      const float* src = &lds.acc[k][hl][e8 * 8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) A[d] = __builtin_fmaf(src[d], w, A[d]);
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void store_out(f16* __restrict__ out, int seq, int h, int n_heads,
+                                          const float (&A)[8], float L) {
+  f16x8 o;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) o[d] = (f16)(A[d] / L);
+  st16(out + ((size_t)seq * n_heads + h) * kHeadDim + (threadIdx.x & 7) * 8, as_u4(o));
+}
+
+__device__ __forceinline__ void store_partial(float* __restrict__ part_o,
+                                              float2* __restrict__ part_ml, size_t slot_idx,
+                                              const float (&A)[8], float M, float L) {
+  float* po = part_o + slot_idx * kHeadDim + (threadIdx.x & 7) * 8;
+  st16(po, u32x4{__builtin_bit_cast(uint32_t, A[0]), __builtin_bit_cast(uint32_t, A[1]),
+                 __builtin_bit_cast(uint32_t, A[2]), __builtin_bit_cast(uint32_t, A[3])});
+  st16(po + 4, u32x4{__builtin_bit_cast(uint32_t, A[4]), __builtin_bit_cast(uint32_t, A[5]),
+                     __builtin_bit_cast(uint32_t, A[6]), __builtin_bit_cast(uint32_t, A[7])});
+  if ((threadIdx.x & 7) == 0) part_ml[slot_idx] = make_float2(M, L);
+}
+
+__device__ __forceinline__ void store_nan(f16* __restrict__ out, int seq, int h, int n_heads) {
+  const u32x4 nan = {0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u};
+  st16(out + ((size_t)seq * n_heads + h) * kHeadDim + (threadIdx.x & 7) * 8, nan);
+}
+
+// Sequence-split grid (num_splits, kv groups, n_seq): block (split, g, s) takes pages
+// [split * pages_per_split, +pages_per_split) of sequence s. Used with one or two splits.
+template <int KVW>
+__global__ void __launch_bounds__(kThreads)
+k_attn_split(const f16* __restrict__ q, const f16* __restrict__ k_pool,
+             const f16* __restrict__ v_pool, const int* __restrict__ block_tables,
+             const int* __restrict__ seq_lens, f16* __restrict__ out, float* __restrict__ part_o,
+             float2* __restrict__ part_ml, int max_pages, int n_heads, int n_kv_heads,
+             int num_splits, int pages_per_split) {
+  __shared__ MergeLds<KVW> lds;
+  const int split = blockIdx.x, kvg = blockIdx.y, seq = blockIdx.z;
+  const int S = seq_lens[seq];
+  const int P = seq_pages(S, max_pages);
+  const int page0 = split * pages_per_split;
+  const int h = kvg * MergeLds<KVW>::HEADS + (threadIdx.x >> 3);
+  const bool writer = (int)(threadIdx.x >> 3) < MergeLds<KVW>::HEADS && h < n_heads;
+  if (page0 >= P) {
+    // No cached position: the quotient 0 / 0 of an all-empty merge, as the reference yields.
+    if (split == 0 && writer) store_nan(out, seq, h, n_heads);
+    return;
+  }
+  const int page1 = page0 + pages_per_split < P ? page0 + pages_per_split : P;
+  const int pos1 = S < page1 * kPage ? S : page1 * kPage;
+  float A[8], M, L;
+  attend_segment<KVW>(q, k_pool, v_pool, block_tables + (size_t)seq * max_pages, seq,
+                      page0 * kPage, pos1, kvg, n_heads, n_kv_heads, lds, A, M, L);
+  if (!writer) return;
+  if ((P + pages_per_split - 1) / pages_per_split == 1)
+    store_out(out, seq, h, n_heads, A, L);
+  else
+    store_partial(part_o, part_ml, ((size_t)seq * num_splits + split) * n_heads + h, A, M, L);
+}
+
+// Sum and maximum of an int over the block (every thread gets both). red: 2 * kWaves ints.
+__device__ __forceinline__ void block_sum_max(int v, int* red, int* sum, int* mx) {
+  int m = v;
+  for (int o = 32; o > 0; o >>= 1) {
+    v += __shfl_xor(v, o);
+    const int t = __shfl_xor(m, o);
+    m = t > m ? t : m;
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[wave] = v;
+    red[kWaves + wave] = m;
+  }
+  __syncthreads();
+  int a = 0, b = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    a += red[w];
+    b = red[kWaves + w] > b ? red[kWaves + w] : b;
+  }
+  *sum = a;
+  *mx = b;
+  __syncthreads();
+}
+
+// Inclusive prefix sum of an int over the block in thread order; *total gets the block's sum.
+__device__ __forceinline__ int block_scan(int v, int* red, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  if (lane == 63) red[wave] = v;
+  __syncthreads();
+  int before = 0, t = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    before += w < wave ? red[w] : 0;
+    t += red[w];
+  }
+  *total = t;
+  __syncthreads();
+  return v + before;
+}
+
+// Sequences whose page counts a thread keeps in registers during the page-balanced prologue;
+// longer batches read the lengths a second time.
+constexpr int kPrologueTiles = 4;
+
+// Page-balanced grid (blocks, kv groups): the pages of all sequences, laid end to end in
+// sequence order (T of them), are cut into runs of q = max(ceil(T / blocks), q_min) pages and
+// block b takes run b, whatever sequences it spans. Every block gets the same amount of work,
+// so one resident round of blocks ends together. Each (sequence, block) piece is a segment; a
+// sequence whose pages start at global page g_s has segments in blocks g_s / q ..
+// (g_s + P_s - 1) / q, and its k-th segment leaves its partial in workspace slot k. q_min =
+// ceil((P_max - 1) / (num_splits - 2)) over the batch's largest page count P_max keeps that
+// count at most num_splits - 1, so slot num_splits - 1 of every sequence is free: the block
+// holding a sequence's first segment records there how many segments it has. A sequence with a
+// single segment gets its output written here; the merge kernel finishes the others and writes
+// the NaN of empty sequences.
+template <int KVW>
+__global__ void __launch_bounds__(kThreads)
+k_attn_balanced(const f16* __restrict__ q, const f16* __restrict__ k_pool,
+                const f16* __restrict__ v_pool, const int* __restrict__ block_tables,
+                const int* __restrict__ seq_lens, f16* __restrict__ out,
+                float* __restrict__ part_o, float2* __restrict__ part_ml, int n_seq,
+                int max_pages, int n_heads, int n_kv_heads, int num_splits) {
+  __shared__ MergeLds<KVW> lds;
+  __shared__ int red[2 * kWaves];
+  __shared__ int found[2];
+  const int b = blockIdx.x, kvg = blockIdx.y, tid = threadIdx.x;
+
+  // Page counts: thread t holds sequences t, t + kThreads, ... (the first kPrologueTiles).
+  const bool held = n_seq <= kPrologueTiles * kThreads;
+  int pv[kPrologueTiles];
+  int mine = 0, pmax = 0;
+#pragma unroll
+  for (int t = 0; t < kPrologueTiles; ++t) {
+    const int s = t * kThreads + tid;
+    pv[t] = s < n_seq ? seq_pages(seq_lens[s], max_pages) : 0;
+    mine += pv[t];
+    pmax = pv[t] > pmax ? pv[t] : pmax;
+  }
+  if (!held)
+    for (int s = kPrologueTiles * kThreads + tid; s < n_seq; s += kThreads) {
+      const int P = seq_pages(seq_lens[s], max_pages);
+      mine += P;
+      pmax = P > pmax ? P : pmax;
+    }
+  int T, P_max;
+  block_sum_max(mine, red, &T, &P_max);
+  const int per = (T + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int q_min = P_max > 1 ? (P_max - 1 + num_splits - 3) / (num_splits - 2) : 1;
+  const int qp = per > q_min ? per : q_min;
+  const long long g0l = (long long)b * qp;
+  if (g0l >= T) return;
+  const int g0 = (int)g0l;
+  const int g1 = g0 + qp < T ? g0 + qp : T;
+
+  // The sequence holding global page g0, and where its pages start.
+  int running = 0;
+  const int tiles = (n_seq + kThreads - 1) / kThreads;
+  for (int t = 0; t < tiles && running <= g0; ++t) {
+    const int s = t * kThreads + tid;
+    int P = 0;
+    if (held) {
+#pragma unroll
+      for (int u = 0; u < kPrologueTiles; ++u) P = u == t ? pv[u] : P;
+    } else {
+      P = s < n_seq ? seq_pages(seq_lens[s], max_pages) : 0;
+    }
+    int tile;
+    const int incl = running + block_scan(P, red, &tile);
+    if (P > 0 && incl - P <= g0 && g0 < incl) {
+      found[0] = s;
+      found[1] = incl - P;
+    }
+    running += tile;
+  }
+  __syncthreads();
+  int s = found[0], gs = found[1];
+
+  const int h = kvg * MergeLds<KVW>::HEADS + (tid >> 3);
+  const bool writer = (tid >> 3) < MergeLds<KVW>::HEADS && h < n_heads;
+  while (gs < g1) {
+    const int S = seq_lens[s];
+    const int P = seq_pages(S, max_pages);
+    if (P > 0) {
+      const int lp0 = (g0 > gs ? g0 : gs) - gs, lp1 = (g1 < gs + P ? g1 : gs + P) - gs;
+      const int pos1 = S < lp1 * kPage ? S : lp1 * kPage;
+      float A[8], M, L;
+      attend_segment<KVW>(q, k_pool, v_pool, block_tables + (size_t)s * max_pages, s,
+                          lp0 * kPage, pos1, kvg, n_heads, n_kv_heads, lds, A, M, L);
+      const int first = gs / qp, n_seg = (gs + P - 1) / qp - first + 1, k = b - first;
+      if (writer) {
+        if (n_seg == 1)
+          store_out(out, s, h, n_heads, A, L);
+        else
+          store_partial(part_o, part_ml, ((size_t)s * num_splits + k) * n_heads + h, A, M, L);
+      }
+      if (k == 0 && tid == 0)
+        part_ml[((size_t)s * num_splits + num_splits - 1) * n_heads] =
+            make_float2(__builtin_bit_cast(float, n_seg), 0.0f);
+    }
+    gs += P;
+    ++s;
+  }
+}
+
+// Grid (ceil(n_heads / 32), n_seq), 256 threads: thread (head, 8 dims). Merges the splits of
+// every sequence that has more than one. pages_per_split > 0: the sequence-split grid's
+// layout, splits = ceil(P / pages_per_split), empty sequences already written. 0: the
+// page-balanced layout, the segment count read from the sequence's last slot. The partials are
+// folded in four at a time, their loads issued together, with a running maximum.
+__global__ void __launch_bounds__(256)
+k_attn_merge(const float* __restrict__ part_o, const float2* __restrict__ part_ml,
+             const int* __restrict__ seq_lens, f16* __restrict__ out, int max_pages, int n_heads,
+             int num_splits, int pages_per_split) {
+  constexpr int kBatch = 4;
+  const int seq = blockIdx.y;
+  const int h = blockIdx.x * 32 + (threadIdx.x >> 3), e8 = threadIdx.x & 7;
+  if (h >= n_heads) return;
+  const size_t base = (size_t)seq * num_splits * n_heads + h;  // slot of split 0
+  // The first batch of slots is loaded together with the length and the segment count; slots
+  // beyond the count hold stale data and are masked below (they lie inside the workspace).
+  float2 ml[kBatch];
+  u32x4 a0[kBatch], a1[kBatch];
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j) {
+    const size_t k = base + (size_t)j * n_heads;
+    const bool in = j < num_splits;
+    ml[j] = in ? part_ml[k] : make_float2(-INFINITY, 0.0f);
+    a0[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8) : zero;
+    a1[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8 + 4) : zero;
+  }
+  const int S = seq_lens[seq];
+  const float2 meta =
+      pages_per_split > 0 ? make_float2(0.0f, 0.0f)
+                          : part_ml[((size_t)seq * num_splits + num_splits - 1) * n_heads];
+  const int P = seq_pages(S, max_pages);
+  int used;
+  if (pages_per_split > 0) {
+    used = (P + pages_per_split - 1) / pages_per_split;
+  } else {
+    if (P == 0) {
+      store_nan(out, seq, h, n_heads);
+      return;
+    }
+    used = __builtin_bit_cast(int, meta.x);
+  }
+  if (used <= 1) return;
+  float M = -INFINITY, L = 0.0f, A[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) A[d] = 0.0f;
+  for (int s0 = 0; s0 < used; s0 += kBatch) {
+    if (s0 > 0) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const size_t k = base + (size_t)(s0 + j) * n_heads;
+        const bool in = s0 + j < used;
+        ml[j] = in ? part_ml[k] : make_float2(-INFINITY, 0.0f);
+        a0[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8) : zero;
+        a1[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8 + 4) : zero;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      if (s0 + j >= used) {  // stale slot (may hold NaN): weight 0 and zero data
+        ml[j] = make_float2(-INFINITY, 0.0f);
+        a0[j] = zero;
+        a1[j] = zero;
+      }
+    float mx = M;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) mx = fmaxf(mx, ml[j].x);
+    const float corr = __builtin_amdgcn_exp2f(M - mx);  // first batch: M = -inf -> 0
+    L = L * corr;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) A[d] = A[d] * corr;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const float w = __builtin_amdgcn_exp2f(ml[j].x - mx);  // masked slot: exp2(-inf) = 0
+      L = __builtin_fmaf(ml[j].y, w, L);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t x0 = elem(a0[j], d), x1 = elem(a1[j], d);
+        A[d] = __builtin_fmaf(__builtin_bit_cast(float, x0), w, A[d]);
+        A[d + 4] = __builtin_fmaf(__builtin_bit_cast(float, x1), w, A[d + 4]);
+      }
+    }
+    M = mx;
+  }
+  store_out(out, seq, h, n_heads, A, L);
+}
+
+// Blocks of k_attn_balanced<KVW> that fit on the device at once (cached per device).
+template <int KVW>
+int resident_blocks() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  const int known = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+  if (known > 0) return known;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, reinterpret_cast<const void*>(k_attn_balanced<KVW>), kThreads, 0) !=
+          hipSuccess)
+    return 0;
+  const int n = cus * (per_cu > 0 ? per_cu : 1);
+  __atomic_store_n(&cache[dev], n, __ATOMIC_RELAXED);
+  return n;
+}
+
+struct AttnArgs {
+  const f16 *q, *k_pool, *v_pool;
+  const int *tables, *lens;
+  f16* out;
+  float* part_o;
+  float2* part_ml;
+  int n_seq, max_pages, n_heads, n_kv_heads, num_splits;
+};
+
+template <int KVW>
+int attn_launch(const AttnArgs& a, hipStream_t s) {
+  const int groups = a.n_kv_heads >= 8 ? a.n_kv_heads / 8 : 1;
+  if (a.num_splits >= 3 && a.part_o) {
+    int blocks = resident_blocks<KVW>() / groups;
+    if (blocks < 1) blocks = 1;
+    int st = launch(k_attn_balanced<KVW>, dim3((unsigned)blocks, (unsigned)groups), dim3(kThreads),
+                    0, s, a.q, a.k_pool, a.v_pool, a.tables, a.lens, a.out, a.part_o, a.part_ml,
+                    a.n_seq, a.max_pages, a.n_heads, a.n_kv_heads, a.num_splits);
+    if (st != 0) return st;
+    const dim3 mgrid((unsigned)((a.n_heads + 31) / 32), (unsigned)a.n_seq);
+    return launch(k_attn_merge, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,
+                  a.max_pages, a.n_heads, a.num_splits, 0);
+  }
+  const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;  // pages per split
+  const dim3 grid((unsigned)a.num_splits, (unsigned)groups, (unsigned)a.n_seq);
+  int st = launch(k_attn_split<KVW>, grid, dim3(kThreads), 0, s, a.q, a.k_pool, a.v_pool,
+                  a.tables, a.lens, a.out, a.part_o, a.part_ml, a.max_pages, a.n_heads,
+                  a.n_kv_heads, a.num_splits, pps);
+  if (st != 0 || pps >= a.max_pages) return st;  // every sequence fits in one split
+  const dim3 mgrid((unsigned)((a.n_heads + 31) / 32), (unsigned)a.n_seq);
+  return launch(k_attn_merge, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,
+                a.max_pages, a.n_heads, a.num_splits, pps);
+}
+
+}  // namespace
+}  // namespace llmk
+
+using namespace llmk;
+
+extern "C" size_t llmk_attention_decode_fast_workspace_floats(int n_seq, int n_heads,
+                                                             int num_splits) {
+  if (n_seq <= 0 || n_heads <= 0 || num_splits <= 0) return 0;
+  return (size_t)n_seq * n_heads * num_splits * (kHeadDim + 2);
+}
+
+extern "C" int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_pool,
+                                          const uint16_t* v_pool, const int32_t* block_tables,
+                                          const int32_t* seq_lens, uint16_t* out,
+                                          float* workspace, int n_seq, int max_pages,
+                                          int page_size, int n_heads, int n_kv_heads,
+                                          int head_dim, int num_splits, void* stream) {
+  if (n_seq == 0) return LLMK_OK;
+  // The reference's preconditions (kernels/attention_decode_fast.cu:160-163).
+  if (page_size != kPage || head_dim != kHeadDim || n_kv_heads <= 0 ||
+      n_heads != kGroup * n_kv_heads)
+    return LLMK_ERR_SHAPE;
+  if (n_seq < 0 || max_pages <= 0 || num_splits <= 0) return LLMK_ERR_INVALID_VALUE;
+  if (n_seq > 65535 || n_kv_heads / 8 > 65535) return LLMK_ERR_UNSUPPORTED;
+  if (!q || !k_pool || !v_pool || !block_tables || !seq_lens || !out)
+    return LLMK_ERR_INVALID_VALUE;
+  if (num_splits > 1 && !workspace) return LLMK_ERR_INVALID_VALUE;
+  if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out) ||
+      (workspace && !aligned16(workspace)))
+    return LLMK_ERR_ALIGNMENT;
+  AttnArgs a;
+  a.q = reinterpret_cast<const f16*>(q);
+  a.k_pool = reinterpret_cast<const f16*>(k_pool);
+  a.v_pool = reinterpret_cast<const f16*>(v_pool);
+  a.tables = block_tables;
+  a.lens = seq_lens;
+  a.out = reinterpret_cast<f16*>(out);
+  a.part_o = workspace;
+  a.part_ml = workspace ? reinterpret_cast<float2*>(
+                              workspace + (size_t)n_seq * num_splits * n_heads * kHeadDim)
+                        : nullptr;
+  a.n_seq = n_seq;
+  a.max_pages = max_pages;
+  a.n_heads = n_heads;
+  a.n_kv_heads = n_kv_heads;
+  a.num_splits = num_splits;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_kv_heads % 8 == 0) return attn_launch<8>(a, s);
+  switch (n_kv_heads) {
+    case 4: return attn_launch<4>(a, s);
+    case 2: return attn_launch<2>(a, s);
+    case 1: return attn_launch<1>(a, s);
+    default: return LLMK_ERR_UNSUPPORTED;  // a row of 3, 5, 6 or 7 kv heads
+  }
+}

@@ -48,10 +48,13 @@ __device__ __forceinline__ u32x4 as_u4(f16x8 v) { return __builtin_bit_cast(u32x
 // (r0 + r1) + (r2 + r3) from lanes 0, 16, 32, 48. Every lane returns the same value. Must be
 // called with all 64 lanes active.
 // ---------------------------------------------------------------------------------------------
+// DPP lane permute for controls whose source lane always exists (quad_perm, row_half_mirror,
+// row_mirror). Written as update_dpp with a zero `old` so that the compiler folds it into the
+// consuming VALU instruction (v_add_f32_dpp) instead of emitting a separate v_mov_b32_dpp.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
   return __builtin_bit_cast(
-      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float readlane_f32(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));

@@ -82,6 +82,21 @@ def bytes_decode_pass(n: int, layers: int) -> int:
     return bytes_embedding(n, HIDDEN) + layers * per_layer
 
 
+def bytes_attention(lens: np.ndarray, nh: int = N_HEADS, nkv: int = N_KV,
+                    hd: int = HEAD_DIM) -> int:
+    """Cached K and V rows of every sequence read once, q read and out written once, plus the
+    page-table entries and lengths read."""
+    lens = np.maximum(np.asarray(lens, np.int64), 0)
+    pages = (lens + PAGE - 1) // PAGE
+    return (int(lens.sum()) * 2 * nkv * hd * 2 + 2 * lens.size * nh * hd * 2
+            + int(pages.sum()) * 4 + lens.size * 4)
+
+
+def attention_lens(n: int = 256, max_len: int = 2048, seed: int = SEED_BASE + 6) -> np.ndarray:
+    """Sequence lengths uniform in [1, max_len] (the decode configuration's context lengths)."""
+    return np.random.default_rng(seed).integers(1, max_len + 1, n)
+
+
 # ---------------------------------------------------------------------------------------------
 # workloads
 # ---------------------------------------------------------------------------------------------
@@ -187,3 +202,39 @@ def decode_pass_inputs(inv_freq: torch.Tensor, n=256, layers=LAYERS, max_pages=1
         block_tables=torch.from_numpy(tables).to(device),
         positions=torch.from_numpy((lens - 1).astype(np.int32)).to(device),
         inv_freq=inv_freq, per_layer=per_layer)
+
+
+def attention_inputs(lens: np.ndarray, max_pages: int = 128, num_splits: int = 32,
+                     seed: int = SEED_BASE + 6, device="cuda") -> dict:
+    """One decode-attention batch: q [n, 32, 64] and the cached K, V rows ~N(0, 1) in pages
+    assigned from a shuffled permutation; the slots past each sequence's length in its last page
+    hold the NaN pattern; a workspace for num_splits splits."""
+    lens = np.asarray(lens, np.int64)
+    n = lens.size
+    rng = np.random.default_rng(seed + 1)
+    npages = (lens + PAGE - 1) // PAGE
+    total = int(npages.sum())
+    perm = rng.permutation(total).astype(np.int32)
+    tables = np.zeros((n, max_pages), np.int32)
+    off = 0
+    for b, p in enumerate(npages):
+        tables[b, :p] = perm[off:off + p]
+        off += p
+    kvdim = N_KV * HEAD_DIM
+    g = _gen(seed, device)
+    k_pool = normal_f16((total * PAGE, kvdim), g, device)
+    v_pool = normal_f16((total * PAGE, kvdim), g, device)
+    tail = [tables[b, npages[b] - 1] * PAGE + j for b in range(n)
+            for j in range(int(lens[b]) % PAGE or PAGE, PAGE)]
+    if tail:
+        idx = torch.tensor(tail, dtype=torch.int64, device=device)
+        k_pool.view(torch.int16).index_fill_(0, idx, POISON)
+        v_pool.view(torch.int16).index_fill_(0, idx, POISON)
+    from . import attention_decode_fast_workspace_floats as ws_floats
+    return dict(q=normal_f16((n, N_HEADS, HEAD_DIM), g, device), k_pool=k_pool.view(-1),
+                v_pool=v_pool.view(-1), block_tables=torch.from_numpy(tables).to(device),
+                seq_lens=torch.from_numpy(lens.astype(np.int32)).to(device),
+                out=torch.empty((n, N_HEADS, HEAD_DIM), dtype=torch.float16, device=device),
+                workspace=torch.empty(ws_floats(n, N_HEADS, num_splits), dtype=torch.float32,
+                                      device=device),
+                n=n, max_pages=max_pages, num_splits=num_splits, total_pages=total)

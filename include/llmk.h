@@ -126,6 +126,41 @@ LLMK_API int llmk_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const ui
                                int max_pages, int page_size, int n_heads, int n_kv_heads,
                                int head_dim, void* stream);
 
+/* Default target block count of choose_num_splits (llmk.hpp) for MI355X. The reference's
+ * default, 64, was fitted to a 20-SM laptop GPU (ref: kernels/attention_decode_fast.cuh:20-22).
+ * Here num_splits only caps how many pieces a sequence may be cut into (libllmk balances the
+ * pages of the whole batch over one resident round of blocks), so the default asks for as many
+ * as the rule allows: 32 for batches up to 256 sequences of 8 kv heads. */
+#define LLMK_ATTN_TARGET_BLOCKS 65536
+
+/* Floats of workspace llmk_attention_decode_fast needs for n_seq sequences, n_heads query
+ * heads and up to num_splits splits per sequence: n_seq * n_heads * num_splits * (64 + 2), the
+ * reference's figure. 0 for non-positive arguments.
+ * ref: kernels/attention_decode_fast.cuh:6, kernels/attention_decode_fast.cu:151-153. */
+LLMK_API size_t llmk_attention_decode_fast_workspace_floats(int n_seq, int n_heads,
+                                                            int num_splits);
+
+/* Batched decode attention over the paged KV cache, one new token per sequence:
+ * out[s, h, :] = softmax_j(q[s, h, :] . K_j / sqrt(head_dim)) . V_j over the positions
+ * j < seq_lens[s], K_j / V_j the pool rows block_tables[s * max_pages + j / page_size] *
+ * page_size + j % page_size, kv head h / (n_heads / n_kv_heads). Layouts: q and out
+ * [n_seq, n_heads, head_dim]; pools [num_pages, page_size, n_kv_heads, head_dim]; block_tables
+ * [n_seq, max_pages]. Requires page_size 16, head_dim 64, n_heads == 4 * n_kv_heads (the
+ * reference's preconditions: LLMK_ERR_SHAPE otherwise) and n_kv_heads a multiple of 8 or one of
+ * 1, 2, 4 (LLMK_ERR_UNSUPPORTED otherwise). Each sequence is cut into at most num_splits runs of
+ * ceil(max_pages / num_splits) pages; with more than one run the partial results go through
+ * `workspace` (llmk_attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits) floats,
+ * 16-byte aligned; may be NULL when num_splits == 1) and a second launch merges them. A
+ * sequence with seq_lens <= 0 gets NaN (the reference's 0 / 0). Positions past max_pages *
+ * page_size are not read. q, pools and out 16-byte aligned.
+ * ref: kernels/attention_decode_fast.cuh:8-18, kernels/attention_decode_fast.cu:155-172. */
+LLMK_API int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_pool,
+                                        const uint16_t* v_pool, const int32_t* block_tables,
+                                        const int32_t* seq_lens, uint16_t* out,
+                                        float* workspace, int n_seq, int max_pages,
+                                        int page_size, int n_heads, int n_kv_heads,
+                                        int head_dim, int num_splits, void* stream);
+
 /* Device-to-device copy of nbytes with 16-byte vector loads and stores, used to measure the
  * practical HBM ceiling and to calibrate rocprof traffic counters. src and dst 16-byte aligned,
  * nbytes % 16 == 0. ref: bench/bandwidth.cu:11-15 (copy_vec4, the reference's bandwidth probe). */

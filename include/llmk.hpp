@@ -123,3 +123,35 @@ inline void rope_kv_scatter_batch(__half* q, const __half* k, const __half* v, _
                                  n_kv_heads, head_dim, stream),
       "rope_kv_scatter_batch");
 }
+
+// ref: kernels/attention_decode_fast.cuh:6
+inline size_t attention_decode_fast_workspace_floats(int n_seq, int n_heads, int num_splits) {
+  return llmk_attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits);
+}
+
+// ref: kernels/attention_decode_fast.cuh:14-18. Preconditions as the reference's (page_size 16,
+// head_dim 64, n_heads == 4 * n_kv_heads): a violation is a fatal host error.
+inline void attention_decode_fast(const __half* q, const __half* k_pool, const __half* v_pool,
+                                  const int* block_tables, const int* seq_lens, __half* out,
+                                  float* workspace, int n_seq, int max_pages, int page_size,
+                                  int n_heads, int n_kv_heads, int head_dim, int num_splits,
+                                  hipStream_t stream = 0) {
+  llmk_shim::check(
+      llmk_attention_decode_fast(llmk_shim::h(q), llmk_shim::h(k_pool), llmk_shim::h(v_pool),
+                                 block_tables, seq_lens, llmk_shim::h(out), workspace, n_seq,
+                                 max_pages, page_size, n_heads, n_kv_heads, head_dim,
+                                 num_splits, stream),
+      "attention_decode_fast");
+}
+
+// The reference's split-count rule (ref: kernels/attention_decode_fast.cuh:22-29), with the
+// default target rescaled for MI355X (LLMK_ATTN_TARGET_BLOCKS).
+inline int choose_num_splits(int n_seq, int n_kv_heads, int max_seq_len,
+                             int target_blocks = LLMK_ATTN_TARGET_BLOCKS) {
+  int splits = target_blocks / (n_seq * n_kv_heads);
+  const int max_splits = (max_seq_len + 15) / 16;  // never more splits than pages
+  if (splits > max_splits) splits = max_splits;
+  if (splits > 32) splits = 32;  // the engine's workspace holds 32 (ref: engine/batched.cu:29)
+  if (splits < 1) splits = 1;
+  return splits;
+}

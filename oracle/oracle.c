@@ -247,6 +247,71 @@ void or_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const uint16_t* v,
   free(kr);
 }
 
+void or_attention_decode_paged(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                               const int32_t* block_tables, const int32_t* seq_lens,
+                               uint16_t* out, int n_seq, int max_pages, int page_size,
+                               int n_heads, int n_kv_heads, int head_dim) {
+  const int group = n_heads / n_kv_heads;
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  const size_t kvrow = (size_t)n_kv_heads * head_dim;
+  int max_s = 1;
+  for (int s = 0; s < n_seq; ++s) max_s = seq_lens[s] > max_s ? seq_lens[s] : max_s;
+  float* sc = (float*)malloc(sizeof(float) * (size_t)max_s);
+  for (int s = 0; s < n_seq; ++s) {
+    const int S = seq_lens[s];
+    const int32_t* table = block_tables + (size_t)s * max_pages;
+    for (int h = 0; h < n_heads; ++h) {
+      const int g = h / group;
+      const uint16_t* qv = q + ((size_t)s * n_heads + h) * head_dim;
+      uint16_t* o = out + ((size_t)s * n_heads + h) * head_dim;
+      if (S <= 0) { /* every split empty: the merge divides 0 by 0 */
+        for (int d = 0; d < head_dim; ++d) o[d] = 0x7E00u;
+        continue;
+      }
+      for (int j = 0; j < S; ++j) {
+        const size_t row = (size_t)table[j / page_size] * page_size + (size_t)(j % page_size);
+        const uint16_t* kv = k_pool + row * kvrow + (size_t)g * head_dim;
+        float dot = 0.0f;
+        for (int d = 0; d < head_dim; ++d) dot = dot + or_h2f(qv[d]) * or_h2f(kv[d]);
+        sc[j] = dot * scale;
+      }
+      float m = -INFINITY;
+      for (int j = 0; j < S; ++j) m = sc[j] > m ? sc[j] : m;
+      float sum = 0.0f;
+      for (int j = 0; j < S; ++j) {
+        sc[j] = (float)exp((double)(sc[j] - m));
+        sum = sum + sc[j];
+      }
+      for (int j = 0; j < S; ++j) sc[j] = sc[j] / sum;
+      for (int d = 0; d < head_dim; ++d) {
+        float acc = 0.0f;
+        for (int j = 0; j < S; ++j) {
+          const size_t row = (size_t)table[j / page_size] * page_size + (size_t)(j % page_size);
+          acc = acc + sc[j] * or_h2f(v_pool[row * kvrow + (size_t)g * head_dim + d]);
+        }
+        o[d] = or_f2h(acc);
+      }
+    }
+  }
+  free(sc);
+}
+
+void or_argmax_rows(const uint16_t* logits, int32_t* out, int n_rows, int n_cols) {
+  for (int r = 0; r < n_rows; ++r) {
+    const uint16_t* row = logits + (size_t)r * n_cols;
+    int best = 0x7FFFFFFF; /* no element above -inf (all -inf or NaN): INT_MAX */
+    float bv = -INFINITY;
+    for (int c = 0; c < n_cols; ++c) {
+      const float v = or_h2f(row[c]);
+      if (v > bv) { /* strictly greater: ties keep the lowest index; NaN never wins */
+        bv = v;
+        best = c;
+      }
+    }
+    out[r] = best;
+  }
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* row-parallel variants (CPU baseline)                                                         */
 /* ------------------------------------------------------------------------------------------ */

@@ -62,6 +62,26 @@ void or_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const uint16_t* v,
                               int max_pages, int page_size, int n_heads, int n_kv_heads,
                               int head_dim);
 
+/* Decode attention over a paged KV cache, one query token per sequence: the arithmetic of
+ * ref: kernels/attention_decode_paged.cu:24-62, the kernel the split-KV kernel
+ * (kernels/attention_decode_fast.cu) is checked against in tests/test_attention_decode_fast.cu:58-61,
+ * applied to every sequence of the batch. For sequence s and query head h, kv head
+ * g = h / (n_heads / n_kv_heads), positions j < seq_lens[s] at pool row
+ * block_tables[s][j / page_size] * page_size + j % page_size: score_j = (sum_d q[d] * k_j[d]) *
+ * (1 / sqrt(head_dim)) in fp32; p_j = exp(score_j - max) / sum_j exp(...); out[d] =
+ * fp16(sum_j p_j * v_j[d]); every sum in fp32, in index order. A sequence with seq_lens <= 0
+ * gets NaN, as the split-KV kernel's merge yields 0 / 0 there
+ * (ref: kernels/attention_decode_fast.cu:42-48, 141-148). */
+void or_attention_decode_paged(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                               const int32_t* block_tables, const int32_t* seq_lens,
+                               uint16_t* out, int n_seq, int max_pages, int page_size,
+                               int n_heads, int n_kv_heads, int head_dim);
+
+/* Row argmax of fp16 logits [n_rows, n_cols] (ref: kernels/argmax.cu:11-40): the index of the
+ * largest value, the lowest index among equal ones (+0 equals -0); NaN never wins; a row with no
+ * value above -inf gives INT_MAX (the reduction's initial index). */
+void or_argmax_rows(const uint16_t* logits, int32_t* out, int n_rows, int n_cols);
+
 /* Row-parallel variants for the CPU baseline: the same per-row code split over nthreads
  * threads by contiguous row ranges (results identical to the single-thread functions). */
 void or_add_rmsnorm_mt(uint16_t* residual, const uint16_t* x, const uint16_t* w, uint16_t* out,

@@ -50,3 +50,67 @@ def shuffled_page_tables(rng: np.random.Generator, lens: np.ndarray, page_size: 
         tables[b, :np_b] = perm[nxt:nxt + np_b]
         nxt += np_b
     return tables, total
+
+
+def uniform_f16(rng: np.random.Generator, shape, lo=-1.0, hi=1.0) -> np.ndarray:
+    """fp16 bit patterns of U(lo, hi) draws, as the reference's attention and argmax tests use."""
+    return rng.uniform(lo, hi, shape).astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+# The shape the reference's split-KV attention is specified for (Llama-3.2-1B,
+# ref: kernels/attention_decode_fast.cuh:13) and its test's sequence lengths, which include the
+# page-boundary cases (ref: tests/test_attention_decode_fast.cu:17-18).
+ATTN = dict(n_heads=32, n_kv_heads=8, head_dim=64, page_size=16)
+ATTN_LENS = (1, 15, 16, 17, 33, 100, 402, 2048)
+
+
+def attention_case(rng: np.random.Generator, lens, n_heads=32, n_kv_heads=8, head_dim=64,
+                   page_size=16, max_pages=None, extra_pages=0):
+    """Inputs laid out as ref: tests/test_attention_decode_fast.cu:22-41: q [n, nh, hd] and the
+    cached K, V rows U(-1, 1); pages assigned from a shuffled permutation; every pool slot that
+    no position uses holds the NaN pattern 0x7F7F. Returns a dict of numpy arrays and sizes."""
+    lens = np.asarray(lens, np.int32)
+    n = lens.size
+    kvdim = n_kv_heads * head_dim
+    npages = (np.maximum(lens, 0) + page_size - 1) // page_size
+    if max_pages is None:
+        max_pages = max(1, int(npages.max()))
+    tables, total = shuffled_page_tables(rng, np.maximum(lens, 0), page_size, max_pages,
+                                         extra_pages)
+    total = max(total, 1)
+    q = uniform_f16(rng, (n, n_heads, head_dim))
+    kp = np.full((total * page_size, kvdim), POISON, np.uint16)
+    vp = kp.copy()
+    for b in range(n):
+        if lens[b] <= 0:
+            continue
+        j = np.arange(lens[b])
+        rows = tables[b, j // page_size] * page_size + j % page_size
+        kp[rows] = uniform_f16(rng, (lens[b], kvdim))
+        vp[rows] = uniform_f16(rng, (lens[b], kvdim))
+    return dict(q=q, k_pool=kp.reshape(-1), v_pool=vp.reshape(-1), tables=tables, lens=lens,
+                n_seq=n, max_pages=max_pages, total_pages=total, n_heads=n_heads,
+                n_kv_heads=n_kv_heads, head_dim=head_dim, page_size=page_size)
+
+
+def attention_f64(case: dict) -> np.ndarray:
+    """Decode attention in float64 with numpy, written from the definition: softmax over the
+    cached positions of q . k / sqrt(head_dim), then the weighted sum of the V rows; query head
+    h reads kv head h // (n_heads / n_kv_heads). Returns float64 [n, nh, hd]."""
+    nh, nkv, hd, ps = case["n_heads"], case["n_kv_heads"], case["head_dim"], case["page_size"]
+    q = case["q"].view(np.float16).astype(np.float64).reshape(case["n_seq"], nh, hd)
+    kp = case["k_pool"].view(np.float16).astype(np.float64).reshape(-1, nkv, hd)
+    vp = case["v_pool"].view(np.float16).astype(np.float64).reshape(-1, nkv, hd)
+    out = np.full((case["n_seq"], nh, hd), np.nan)
+    for b, S in enumerate(case["lens"]):
+        if S <= 0:
+            continue
+        j = np.arange(S)
+        rows = case["tables"][b, j // ps] * ps + j % ps
+        K, V = kp[rows], vp[rows]  # [S, nkv, hd]
+        for h in range(nh):
+            g = h // (nh // nkv)
+            s = K[:, g, :] @ q[b, h] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            out[b, h] = (p / p.sum()) @ V[:, g, :]
+    return out

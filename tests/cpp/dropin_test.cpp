@@ -257,6 +257,69 @@ int main() {
     (void)hipFree(dpos); (void)hipFree(dqb); (void)hipFree(dvb); (void)hipFree(dvp); (void)hipFree(dinv);
   }
 
+  // ---- attention_decode_fast (ref: tests/test_attention_decode_fast.cu:16-99): its lengths,
+  // shuffled pages, NaN in every unused slot, the output memset to 0x7F, and one run per split
+  // count with a workspace sized by attention_decode_fast_workspace_floats.
+  {
+    const int NH = 32, NKV = 8, HD = 64, P = 16, kvdim = NKV * HD;
+    const std::vector<int> lens = {1, 15, 16, 17, 33, 100, 402, 2048};
+    const int n_seq = (int)lens.size();
+    int max_pages = 0, total_pages = 0;
+    for (int S : lens) {
+      const int np = (S + P - 1) / P;
+      max_pages = std::max(max_pages, np);
+      total_pages += np;
+    }
+    std::mt19937 rng(2024);
+    std::uniform_real_distribution<float> U(-1.f, 1.f);
+    std::vector<uint16_t> q((size_t)n_seq * NH * HD);
+    for (auto& x : q) x = or_f2h(U(rng));
+    std::vector<int> perm(total_pages);
+    std::iota(perm.begin(), perm.end(), 0);
+    std::shuffle(perm.begin(), perm.end(), rng);
+    std::vector<int> tables((size_t)n_seq * max_pages, 0);
+    std::vector<uint16_t> kp((size_t)total_pages * P * kvdim, 0x7F7F), vp(kp.size(), 0x7F7F);
+    int next = 0;
+    for (int s = 0; s < n_seq; s++) {
+      const int np = (lens[s] + P - 1) / P;
+      for (int i = 0; i < np; i++) tables[(size_t)s * max_pages + i] = perm[next++];
+      for (int j = 0; j < lens[s]; j++) {
+        const size_t dst = ((size_t)tables[(size_t)s * max_pages + j / P] * P + j % P) * kvdim;
+        for (int d = 0; d < kvdim; d++) {
+          kp[dst + d] = or_f2h(U(rng));
+          vp[dst + d] = or_f2h(U(rng));
+        }
+      }
+    }
+    std::vector<uint16_t> expected(q.size());
+    or_attention_decode_paged(q.data(), kp.data(), vp.data(), tables.data(), lens.data(),
+                              expected.data(), n_seq, max_pages, P, NH, NKV, HD);
+    uint16_t *dq = to_dev(q), *dk = to_dev(kp), *dv = to_dev(vp);
+    uint16_t* dout = to_dev(std::vector<uint16_t>(), q.size());
+    int *dtab = to_dev(tables), *dlens = to_dev(lens);
+    for (int splits : {1, 2, 3, 8, 16, 32}) {
+      float* dws = nullptr;
+      HIP_CHECK(hipMalloc(&dws, attention_decode_fast_workspace_floats(n_seq, NH, splits) *
+                                    sizeof(float)));
+      HIP_CHECK(hipMemset(dout, 0x7F, q.size() * 2));
+      attention_decode_fast(reinterpret_cast<__half*>(dq), reinterpret_cast<__half*>(dk),
+                            reinterpret_cast<__half*>(dv), dtab, dlens,
+                            reinterpret_cast<__half*>(dout), dws, n_seq, max_pages, P, NH, NKV,
+                            HD, splits);
+      HIP_CHECK(hipGetLastError());
+      HIP_CHECK(hipDeviceSynchronize());
+      const bool ok = within_tol(to_host(dout, q.size()), expected, detail, sizeof detail);
+      char name[64];
+      std::snprintf(name, sizeof name, "attention_decode_fast splits %d", splits);
+      report(name, ok, detail);
+      (void)hipFree(dws);
+    }
+    const int pick = choose_num_splits(256, NKV, 2048);
+    report("choose_num_splits MI355X default", pick == 32);
+    (void)hipFree(dq); (void)hipFree(dk); (void)hipFree(dv); (void)hipFree(dout);
+    (void)hipFree(dtab); (void)hipFree(dlens);
+  }
+
   std::printf("%s: %d failure(s)\n", failures ? "FAILED" : "ALL PASSED", failures);
   return failures;
 }

@@ -105,6 +105,33 @@ def test_argument_validation_without_launch(llmk):
                                         32, 8, 64, None) == E.LLMK_ERR_ALIGNMENT
     assert L.llmk_copy_bytes(MIS, FAKE, 32, None) == E.LLMK_ERR_ALIGNMENT
     assert L.llmk_compute_rope_inv_freq(63, 1e4, 1, 1, 4, 8192, None) == E.LLMK_ERR_INVALID_VALUE
+    # split-KV attention: the reference's preconditions (kernels/attention_decode_fast.cu:160-163)
+    A = L.llmk_attention_decode_fast
+    assert A(None, None, None, None, None, None, None, 0, 8, 16, 32, 8, 64, 4, None) == 0
+    assert A(*[FAKE] * 7, 4, 8, 32, 32, 8, 64, 4, None) == E.LLMK_ERR_SHAPE
+    assert A(*[FAKE] * 7, 4, 8, 16, 32, 8, 128, 4, None) == E.LLMK_ERR_SHAPE
+    assert A(*[FAKE] * 7, 4, 8, 16, 24, 8, 64, 4, None) == E.LLMK_ERR_SHAPE
+    assert A(*[FAKE] * 7, 4, 8, 16, 12, 3, 64, 4, None) == E.LLMK_ERR_UNSUPPORTED
+    assert A(*[FAKE] * 7, 4, 8, 16, 32, 8, 64, 0, None) == E.LLMK_ERR_INVALID_VALUE
+    assert A(*[FAKE] * 6, None, 4, 8, 16, 32, 8, 64, 2, None) == E.LLMK_ERR_INVALID_VALUE
+    assert A(MIS, *[FAKE] * 6, 4, 8, 16, 32, 8, 64, 2, None) == E.LLMK_ERR_ALIGNMENT
+    assert L.llmk_attention_decode_fast_workspace_floats(256, 32, 32) == 256 * 32 * 32 * 66
+    assert L.llmk_attention_decode_fast_workspace_floats(0, 32, 32) == 0
+
+
+def test_split_count_rule_and_its_default(llmk):
+    """choose_num_splits restates the reference's rule (kernels/attention_decode_fast.cuh:22-29);
+    the Python default equals LLMK_ATTN_TARGET_BLOCKS of the C header."""
+    import re
+    with open(llmk.HEADER_PATH) as f:
+        m = re.search(r"#define LLMK_ATTN_TARGET_BLOCKS (\d+)", f.read())
+    assert m and int(m.group(1)) == llmk.ATTN_TARGET_BLOCKS
+    assert llmk.choose_num_splits(16, 8, 2048, 64) == 1  # reference defaults: 64 // 128 -> 0 -> 1
+    assert llmk.choose_num_splits(2, 8, 2048, 64) == 4
+    assert llmk.choose_num_splits(1, 8, 30, 64) == 2    # capped by the page count
+    assert llmk.choose_num_splits(1, 1, 4096, 64) == 32  # capped at 32
+    assert llmk.choose_num_splits(256, 8, 2048) == 32
+    assert llmk.choose_num_splits(1024, 8, 2048) == 8
 
 
 def test_python_wrapper_rejects_host_tensors_and_short_buffers(llmk):

@@ -8,7 +8,8 @@ criteria used here reject plausible mistakes (a dropped rounding step, a wrong p
 import numpy as np
 import pytest
 
-from _helpers import EPS, POISON, ROPE, assert_tol, goldens, normal_f16, shuffled_page_tables
+from _helpers import (ATTN_LENS, EPS, POISON, ROPE, assert_tol, attention_case, attention_f64,
+                      goldens, normal_f16, shuffled_page_tables, uniform_f16)
 
 
 def f16(bits):
@@ -374,3 +375,146 @@ def test_threaded_variants_equal_single_thread(orc):
     ids = rng.integers(0, 100, 53).astype(np.int32)
     assert np.array_equal(orc.embedding_lookup(table, ids, 256),
                           orc.embedding_lookup(table, ids, 256, threads=3))
+
+
+# --------------------------------------------------------------------------------------------
+# decode attention over the paged pool
+# --------------------------------------------------------------------------------------------
+def _attend(orc, c):
+    return orc.attention_decode_paged(c["q"], c["k_pool"], c["v_pool"], c["tables"], c["lens"],
+                                      c["n_seq"], c["max_pages"], c["page_size"], c["n_heads"],
+                                      c["n_kv_heads"], c["head_dim"])
+
+
+def test_attention_matches_float64_definition(orc):
+    """The reference test's lengths and U(-1, 1) data: within the reference's tolerance of a
+    float64 evaluation from the definition, nearly always its fp16 rounding exactly."""
+    c = attention_case(np.random.default_rng(20), ATTN_LENS)
+    ref = attention_f64(c).astype(np.float16).view(np.uint16)
+    assert_tol(orc.compare(_attend(orc, c), ref), 0.97, "oracle attention vs float64")
+
+
+def test_attention_grouped_query_mapping_and_scale_are_pinned(orc):
+    """Two plausible mistakes fail the float64 check: query head h reading kv head h % n_kv
+    instead of h // (n_heads / n_kv), and a score scale of 1 / head_dim instead of
+    1 / sqrt(head_dim)."""
+    c = attention_case(np.random.default_rng(21), (5, 40, 300))
+    got = _attend(orc, c)
+    nh, nkv, hd, ps = 32, 8, 64, 16
+    q = c["q"].view(np.float16).astype(np.float64).reshape(-1, nh, hd)
+    kp = c["k_pool"].view(np.float16).astype(np.float64).reshape(-1, nkv, hd)
+    vp = c["v_pool"].view(np.float16).astype(np.float64).reshape(-1, nkv, hd)
+
+    def variant(kv_of, scale):
+        out = np.empty_like(q)
+        for b, S in enumerate(c["lens"]):
+            j = np.arange(S)
+            rows = c["tables"][b, j // ps] * ps + j % ps
+            for h in range(nh):
+                s = kp[rows, kv_of(h)] @ q[b, h] * scale
+                p = np.exp(s - s.max())
+                out[b, h] = (p / p.sum()) @ vp[rows, kv_of(h)]
+        return out.astype(np.float16).view(np.uint16)
+
+    assert orc.compare(got, variant(lambda h: h // 4, 0.125))["bad"] == 0
+    assert orc.compare(got, variant(lambda h: h % nkv, 0.125))["bad"] > 0
+    assert orc.compare(got, variant(lambda h: h // 4, 1.0 / 64))["bad"] > 0
+
+
+def test_attention_single_position_returns_its_value_row(orc):
+    """With one cached position the softmax weight is exactly 1: out = V row, bit for bit."""
+    c = attention_case(np.random.default_rng(22), (1, 1, 1))
+    got = _attend(orc, c).reshape(3, 32, 64)
+    rows = c["tables"][:, 0] * 16
+    v = c["v_pool"].reshape(-1, 8, 64)[rows]  # [3, nkv, hd]
+    assert np.array_equal(got, np.repeat(v, 4, axis=1))
+
+
+def test_attention_equal_keys_average_the_values(orc):
+    """Identical K rows give uniform weights: out = mean of the V rows."""
+    rng = np.random.default_rng(23)
+    c = attention_case(rng, (37, 200))
+    kp = c["k_pool"].reshape(-1, 512)
+    kp[:] = uniform_f16(rng, 512)[None, :]
+    ref = np.empty((2, 32, 64))
+    vp = c["v_pool"].view(np.float16).astype(np.float64).reshape(-1, 8, 64)
+    for b, S in enumerate(c["lens"]):
+        j = np.arange(S)
+        rows = c["tables"][b, j // 16] * 16 + j % 16
+        ref[b] = np.repeat(vp[rows].mean(axis=0), 4, axis=0)
+    assert_tol(orc.compare(_attend(orc, c), ref.astype(np.float16).view(np.uint16)), 0.9,
+               "uniform weights")
+
+
+def test_attention_page_placement_does_not_change_results(orc):
+    """The same per-position data placed in shuffled pages or in pages 0, 1, 2, ... gives
+    bit-identical outputs: only the position order enters the sums."""
+    rng = np.random.default_rng(24)
+    c = attention_case(rng, (50, 129, 16))
+    got = _attend(orc, c)
+    d = dict(c)
+    kv = {}
+    for name in ("k_pool", "v_pool"):
+        pool = c[name].reshape(-1, 512)
+        flat = np.full_like(pool, POISON)
+        nxt = 0
+        tables = np.zeros_like(c["tables"])
+        for b, S in enumerate(c["lens"]):
+            npg = (S + 15) // 16
+            tables[b, :npg] = np.arange(nxt, nxt + npg)
+            for i in range(npg):
+                flat[(nxt + i) * 16:(nxt + i + 1) * 16] = pool[c["tables"][b, i] * 16:
+                                                              (c["tables"][b, i] + 1) * 16]
+            nxt += npg
+        kv[name] = flat.reshape(-1)
+    d.update(kv, tables=tables)
+    assert np.array_equal(_attend(orc, d), got)
+
+
+def test_attention_empty_sequence_is_nan(orc):
+    c = attention_case(np.random.default_rng(25), (0, 3))
+    got = _attend(orc, c).reshape(2, -1).view(np.float16)
+    assert np.all(np.isnan(got[0])) and np.all(np.isfinite(got[1]))
+
+
+# --------------------------------------------------------------------------------------------
+# argmax over logits rows
+# --------------------------------------------------------------------------------------------
+def argmax_reference_rows(rng, V=128256):
+    """The rows of ref: tests/test_argmax.cu:10-25: four rows of many exact ties, a constant
+    row, the maximum at the last index, two equal maxima at 0 and 77777, a random row."""
+    rows = np.empty((8, V), np.float32)
+    rows[:4] = rng.integers(-8, 9, (4, V)) * 0.5
+    rows[4] = 1.0
+    rows[5:] = rng.uniform(-5, 5, (3, V))
+    rows[5, V - 1] = 100.0
+    rows[6, 0] = rows[6, 77777] = 100.0
+    return rows.astype(np.float16).view(np.uint16)
+
+
+def test_argmax_reference_rows_match_numpy(orc):
+    rows = argmax_reference_rows(np.random.default_rng(3))
+    got = orc.argmax_rows(rows, 8, rows.shape[1])
+    assert np.array_equal(got, np.argmax(rows.view(np.float16), axis=1))  # first maximum
+    assert got[4] == 0 and got[5] == rows.shape[1] - 1 and got[6] == 0
+
+
+def test_argmax_nan_inf_and_signed_zero(orc):
+    nan, inf = np.float16(np.nan), np.float16(np.inf)
+    rows = np.array([[nan, 1, 3, nan, 3],        # NaN never wins: first 3
+                     [nan, nan, nan, nan, nan],   # nothing above -inf: INT_MAX
+                     [-inf, -inf, -inf, -inf, -inf],
+                     [-0.0, 0.0, -0.0, -1, -2],   # +0 == -0: the first zero
+                     [-inf, -inf, -60000, nan, -inf],
+                     [inf, 1, inf, 2, nan]], np.float16)
+    got = orc.argmax_rows(rows.view(np.uint16), rows.shape[0], rows.shape[1])
+    assert list(got) == [2, 0x7FFFFFFF, 0x7FFFFFFF, 0, 2, 0]
+    finite_rows = [0, 3, 4, 5]
+    assert np.array_equal(got[finite_rows], np.nanargmax(rows[finite_rows], axis=1))
+
+
+def test_mutant_argmax_last_index_on_ties_is_caught(orc):
+    """Keeping the last of equal maxima (>= instead of >) fails the reference's tie rows."""
+    rows = argmax_reference_rows(np.random.default_rng(3)).view(np.float16)
+    last = rows.shape[1] - 1 - np.argmax(rows[:, ::-1], axis=1)
+    assert not np.array_equal(orc.argmax_rows(rows.view(np.uint16), 8, rows.shape[1]), last)
