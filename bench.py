@@ -89,6 +89,7 @@ PROFILE_SHAPES = [
      ("k_attn_merge", 256 * 256)),
     ("attention_decode_16x2048", "k_attn_balancedILi8E", 1024 * 256, ATTN_BYTES_16x2048,
      ("k_attn_merge", 256 * 16)),
+    ("argmax_256x128256", "k_argmax_vec", 256 * 1024, 256 * 128256 * 2 + 256 * 4),
     ("decode:embedding_256", "k_embeddingILi0E", 256 * 64, 2098176),
     ("decode:add_rmsnorm_256x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 256 * 64, 4198400),
     ("decode:rope_kv_scatter_256", "k_rope_vecILi4ELi2ELb1E", 256 * 256, 3147904),
@@ -423,6 +424,21 @@ def main() -> int:
                                      "launches": 2, "note": "page-balanced split + merge"})
             del sets6
             torch.cuda.empty_cache()
+
+        # argmax over the logits of a decode batch: [256, 128256] (ref: kernels/argmax.cu,
+        # engine/batched.cu:150). 17 sets of 65.7 MB rotate through more than 1 GB.
+        R7, n7 = 17, 256
+        g7 = torch.Generator(device=dev)
+        g7.manual_seed(wl.SEED_BASE + 7)
+        logits = [torch.randn((n7, wl.VOCAB), generator=g7, device=dev).half()
+                  for _ in range(R7)]
+        am_out = torch.empty(n7, dtype=torch.int32, device=dev)
+        t = timer.run(lambda i: llmk.argmax_rows(logits[i], am_out, n7, wl.VOCAB), R7, K, W)
+        kernels["argmax_256x128256"] = kernel_entry(
+            "argmax_rows [256,128256]", wl.bytes_argmax(n7, wl.VOCAB), t,
+            traffic.get("argmax_256x128256"), {"sets": R7})
+        del logits
+        torch.cuda.empty_cache()
 
         # copy probe: practical HBM ceiling (ref: bench/bandwidth.cu)
         nb = 1 << 30

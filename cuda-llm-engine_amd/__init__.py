@@ -82,6 +82,7 @@ _SIGS = {
     "llmk_rope_kv_scatter_batch": (_i, [_vp] * 8 + [_i] * 6 + [_vp]),
     "llmk_copy_bytes": (_i, [_vp, _vp, _sz, _vp]),
     "llmk_attention_decode_fast_workspace_floats": (_sz, [_i, _i, _i]),
+    "llmk_argmax_rows": (_i, [_vp, _vp, _i, _i, _vp]),
     "llmk_attention_decode_fast": (_i, [_vp] * 7 + [_i] * 7 + [_vp]),
     "llmk_decode_nongemm_pass": (_i, [ctypes.POINTER(DecodePass), _vp]),
 }
@@ -351,6 +352,17 @@ def attention_decode_fast(q, k_pool, v_pool, block_tables, seq_lens, out, worksp
     _check(fn, _lib.llmk_attention_decode_fast(pq, pk, pv, pt, pl, po, pw, n_seq, max_pages,
                                                page_size, n_heads, n_kv_heads, head_dim,
                                                num_splits, _stream(stream)))
+
+
+def argmax_rows(logits, out, n_rows: int, vocab: int, stream=None) -> None:
+    """out[r] = index of the largest value of row r, lowest index on ties
+    (ref: kernels/argmax.cuh:5-7)."""
+    fn = "argmax_rows"
+    if n_rows < 0 or vocab <= 0:
+        _fail(fn, "n_rows must be >= 0 and vocab > 0")
+    pl = _dev(fn, logits, torch.float16, n_rows * vocab, "logits")
+    po = _dev(fn, out, torch.int32, n_rows, "out")
+    _check(fn, _lib.llmk_argmax_rows(pl, po, n_rows, vocab, _stream(stream)))
 
 
 def copy_bytes(src, dst, nbytes: int, stream=None) -> None:

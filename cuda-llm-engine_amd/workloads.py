@@ -92,6 +92,10 @@ def bytes_attention(lens: np.ndarray, nh: int = N_HEADS, nkv: int = N_KV,
             + int(pages.sum()) * 4 + lens.size * 4)
 
 
+def bytes_argmax(n: int, vocab: int) -> int:
+    return n * vocab * 2 + n * 4  # logits read once, one int32 per row written
+
+
 def attention_lens(n: int = 256, max_len: int = 2048, seed: int = SEED_BASE + 6) -> np.ndarray:
     """Sequence lengths uniform in [1, max_len] (the decode configuration's context lengths)."""
     return np.random.default_rng(seed).integers(1, max_len + 1, n)

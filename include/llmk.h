@@ -161,6 +161,14 @@ LLMK_API int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_poo
                                         int page_size, int n_heads, int n_kv_heads,
                                         int head_dim, int num_splits, void* stream);
 
+/* Row argmax of fp16 logits [n_rows, vocab]: out[r] = the index of the largest value of row r,
+ * the lowest index among equal values (+0 equals -0); NaN is never chosen; a row with no value
+ * above -inf gives INT_MAX. Any vocab and alignment (16-byte vector path when vocab % 8 == 0,
+ * the rows are 16-byte aligned and vocab >= 8192).
+ * ref: kernels/argmax.cuh:5-7, kernels/argmax.cu:5-44. */
+LLMK_API int llmk_argmax_rows(const uint16_t* logits, int32_t* out, int n_rows, int vocab,
+                              void* stream);
+
 /* Device-to-device copy of nbytes with 16-byte vector loads and stores, used to measure the
  * practical HBM ceiling and to calibrate rocprof traffic counters. src and dst 16-byte aligned,
  * nbytes % 16 == 0. ref: bench/bandwidth.cu:11-15 (copy_vec4, the reference's bandwidth probe). */

@@ -155,3 +155,10 @@ inline int choose_num_splits(int n_seq, int n_kv_heads, int max_seq_len,
   if (splits < 1) splits = 1;
   return splits;
 }
+
+// ref: kernels/argmax.cuh:7
+inline void argmax_rows(const __half* logits, int* out, int n_rows, int vocab,
+                        hipStream_t stream = 0) {
+  llmk_shim::check(llmk_argmax_rows(llmk_shim::h(logits), out, n_rows, vocab, stream),
+                   "argmax_rows");
+}

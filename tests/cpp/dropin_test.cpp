@@ -320,6 +320,42 @@ int main() {
     (void)hipFree(dtab); (void)hipFree(dlens);
   }
 
+  // ---- argmax_rows (ref: tests/test_argmax.cu:9-46): 8 rows of 128256 -- four rows of exact
+  // ties, a constant row (answer 0), the maximum at the last index, two equal maxima at 0 and
+  // 77777 (answer 0), a random row.
+  {
+    const int V = 128256, R = 8;
+    std::mt19937 rng(3);
+    std::uniform_real_distribution<float> U(-5.f, 5.f);
+    std::uniform_int_distribution<int> small(-8, 8);
+    std::vector<uint16_t> h((size_t)R * V);
+    for (int r = 0; r < R; r++)
+      for (int i = 0; i < V; i++) {
+        float v;
+        if (r < 4) v = small(rng) * 0.5f;
+        else if (r == 4) v = 1.0f;
+        else v = U(rng);
+        h[(size_t)r * V + i] = or_f2h(v);
+      }
+    h[(size_t)5 * V + (V - 1)] = or_f2h(100.f);
+    h[(size_t)6 * V + 0] = or_f2h(100.f);
+    h[(size_t)6 * V + 77777] = or_f2h(100.f);
+    std::vector<int32_t> expected(R);
+    or_argmax_rows(h.data(), expected.data(), R, V);
+    uint16_t* d = to_dev(h);
+    int* dout = to_dev(std::vector<int>(R, -1));
+    argmax_rows(reinterpret_cast<__half*>(d), dout, R, V);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipDeviceSynchronize());
+    const std::vector<int> got = to_host(dout, R);
+    bool ok = true;
+    for (int r = 0; r < R; r++) ok = ok && got[r] == expected[r];
+    report("argmax_rows exact (reference rows)", ok);
+    report("argmax_rows constant row -> 0, tie -> 0, last", got[4] == 0 && got[6] == 0 &&
+                                                               got[5] == V - 1);
+    (void)hipFree(d); (void)hipFree(dout);
+  }
+
   std::printf("%s: %d failure(s)\n", failures ? "FAILED" : "ALL PASSED", failures);
   return failures;
 }

@@ -117,6 +117,9 @@ def test_argument_validation_without_launch(llmk):
     assert A(MIS, *[FAKE] * 6, 4, 8, 16, 32, 8, 64, 2, None) == E.LLMK_ERR_ALIGNMENT
     assert L.llmk_attention_decode_fast_workspace_floats(256, 32, 32) == 256 * 32 * 32 * 66
     assert L.llmk_attention_decode_fast_workspace_floats(0, 32, 32) == 0
+    assert L.llmk_argmax_rows(None, None, 0, 128256, None) == 0
+    assert L.llmk_argmax_rows(FAKE, FAKE, 4, 0, None) == E.LLMK_ERR_INVALID_VALUE
+    assert L.llmk_argmax_rows(None, FAKE, 4, 100, None) == E.LLMK_ERR_INVALID_VALUE
 
 
 def test_split_count_rule_and_its_default(llmk):
