@@ -30,6 +30,8 @@ LLMK_ERR_INVALID_VALUE = 10001
 LLMK_ERR_SHAPE = 10002
 LLMK_ERR_ALIGNMENT = 10003
 LLMK_ERR_UNSUPPORTED = 10004
+LLMK_ERR_BLAS = 10005
+LLMK_ERR_IO = 10006
 
 
 class LlmkError(RuntimeError):
@@ -67,6 +69,37 @@ class DecodePass(ctypes.Structure):
     ]
 
 
+class ModelConfig(ctypes.Structure):
+    """Mirror of ``struct llmk_model_config`` (include/llmk.h). Defaults: Llama-3.2-1B
+    (ref: engine/layer.h:6-9, engine/model.h:7, engine/model.cu:20)."""
+    _fields_ = [
+        ("n_layers", _i), ("hidden", _i), ("n_heads", _i), ("n_kv_heads", _i),
+        ("head_dim", _i), ("inter", _i), ("vocab", _i), ("eps", _f),
+        ("rope_theta", _d), ("rope_factor", _d), ("rope_low_freq_factor", _d),
+        ("rope_high_freq_factor", _d), ("rope_original_max_pos", _d),
+    ]
+
+    def __init__(self, **kw):
+        base = dict(n_layers=16, hidden=2048, n_heads=32, n_kv_heads=8, head_dim=64,
+                    inter=8192, vocab=128256, eps=1e-5, rope_theta=500000.0, rope_factor=32.0,
+                    rope_low_freq_factor=1.0, rope_high_freq_factor=4.0,
+                    rope_original_max_pos=8192.0)
+        unknown = set(kw) - set(base)
+        if unknown:
+            raise TypeError(f"unknown ModelConfig fields {sorted(unknown)}")
+        base.update(kw)
+        super().__init__(**base)
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class LayerWeights(ctypes.Structure):
+    """Mirror of ``struct llmk_layer_weights`` (ref: engine/layer.h:11-13)."""
+    NAMES = ("attn_norm", "wq", "wk", "wv", "wo", "mlp_norm", "w_gate", "w_up", "w_down")
+    _fields_ = [(n, _vp) for n in NAMES]
+
+
 _SIGS = {
     "llmk_error_string": (ctypes.c_char_p, [_i]),
     "llmk_version": (_i, []),
@@ -85,6 +118,19 @@ _SIGS = {
     "llmk_argmax_rows": (_i, [_vp, _vp, _i, _i, _vp]),
     "llmk_attention_decode_fast": (_i, [_vp] * 7 + [_i] * 7 + [_vp]),
     "llmk_decode_nongemm_pass": (_i, [ctypes.POINTER(DecodePass), _vp]),
+    "llmk_blas_create": (_i, [ctypes.POINTER(_vp)]),
+    "llmk_blas_destroy": (None, [_vp]),
+    "llmk_linear": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "llmk_qkv_rope_scatter": (_i, [_vp, _i] + [_vp] * 6 + [_i] * 6 + [_vp]),
+    "llmk_swiglu_rows": (_i, [_vp, _vp, _i, _i, _vp]),
+    "llmk_engine_create": (_i, [ctypes.POINTER(ModelConfig), _i, _i, _i, ctypes.POINTER(_vp)]),
+    "llmk_engine_destroy": (None, [_vp]),
+    "llmk_engine_set_weights": (_i, [_vp, _vp, _vp, ctypes.POINTER(LayerWeights)]),
+    "llmk_engine_load_weights": (_i, [_vp, ctypes.c_char_p]),
+    "llmk_engine_set_rows": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp]),
+    "llmk_engine_forward": (_i, [_vp, _i, _i, _i, _vp]),
+    "llmk_engine_buffer": (_vp, [_vp, _i, _i]),
+    "llmk_engine_reset_pools": (_i, [_vp, _vp]),
 }
 
 _lib = ctypes.CDLL(LIB_PATH)
@@ -426,3 +472,224 @@ class DecodeNonGemmPass:
     def run(self, stream=None) -> None:
         _check("decode_nongemm_pass",
                _lib.llmk_decode_nongemm_pass(ctypes.byref(self._desc), _stream(stream)))
+
+
+# ---------------------------------------------------------------------------------------------
+# the decode step: projections, fused layouts, engine
+# ---------------------------------------------------------------------------------------------
+class Blas:
+    """A GEMM handle (``llmk_blas``): hipBLASLt handle, 32 MiB workspace, per-shape plans.
+    Stands where the reference passes a cublasHandle_t (ref: kernels/linear.cuh:7)."""
+
+    def __init__(self):
+        h = _vp()
+        _check("blas_create", _lib.llmk_blas_create(ctypes.byref(h)))
+        self._h = h
+
+    @property
+    def handle(self) -> int:
+        return self._h.value
+
+    def close(self) -> None:
+        if self._h:
+            _lib.llmk_blas_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def linear(handle: Blas, x, w, y, T: int, in_features: int, out_features: int,
+           stream=None) -> None:
+    """y[T, out] = x[T, in] W^T, W [out, in] row-major (ref: kernels/linear.cuh:5-7)."""
+    fn = "linear"
+    if T < 0 or in_features <= 0 or out_features <= 0:
+        _fail(fn, "T must be >= 0 and the feature counts > 0")
+    px = _dev(fn, x, torch.float16, T * in_features, "x")
+    pw = _dev(fn, w, torch.float16, out_features * in_features, "w")
+    py = _dev(fn, y, torch.float16, T * out_features, "y")
+    _check(fn, _lib.llmk_linear(handle.handle, px, pw, py, T, in_features, out_features,
+                                _stream(stream)))
+
+
+def qkv_rope_scatter(qkv, ld: int, q_out, k_pool, v_pool, block_tables, positions, inv_freq,
+                     n: int, max_pages: int, page_size: int, n_heads: int, n_kv_heads: int,
+                     head_dim: int, stream=None, check_indices: bool = True) -> None:
+    """RoPE + KV scatter from the rows of a fused QKV projection (``llmk_qkv_rope_scatter``)."""
+    fn = "qkv_rope_scatter"
+    kvdim = n_kv_heads * head_dim
+    if n < 0 or ld < (n_heads + 2 * n_kv_heads) * head_dim:
+        _fail(fn, "n must be >= 0 and ld >= (n_heads + 2 n_kv_heads) head_dim")
+    width = (n_heads + 2 * n_kv_heads) * head_dim
+    pqkv = _dev(fn, qkv, torch.float16, (n - 1) * ld + width if n else 0, "qkv")
+    pq = _dev(fn, q_out, torch.float16, n * n_heads * head_dim, "q_out")
+    pk = _dev(fn, k_pool, torch.float16, 0, "k_pool")
+    pv = _dev(fn, v_pool, torch.float16, 0, "v_pool")
+    pt = _dev(fn, block_tables, torch.int32, n * max_pages, "block_tables")
+    pp = _dev(fn, positions, torch.int32, n, "positions")
+    pi = _dev(fn, inv_freq, torch.float32, head_dim // 2, "inv_freq")
+    if check_indices and n > 0:
+        _check_batch_tables(fn, block_tables, positions, [k_pool, v_pool], n, max_pages,
+                            page_size, kvdim)
+    _check(fn, _lib.llmk_qkv_rope_scatter(pqkv, ld, pq, pk, pv, pt, pp, pi, n, max_pages,
+                                          page_size, n_heads, n_kv_heads, head_dim,
+                                          _stream(stream)))
+
+
+def swiglu_rows(gate_up, out, n_rows: int, inter: int, stream=None) -> None:
+    """out[r] = swiglu(gate_up[r, :inter], gate_up[r, inter:]) (``llmk_swiglu_rows``)."""
+    fn = "swiglu_rows"
+    if n_rows < 0 or inter <= 0:
+        _fail(fn, "n_rows must be >= 0 and inter > 0")
+    pg = _dev(fn, gate_up, torch.float16, n_rows * 2 * inter, "gate_up")
+    po = _dev(fn, out, torch.float16, n_rows * inter, "out")
+    _check(fn, _lib.llmk_swiglu_rows(pg, po, n_rows, inter, _stream(stream)))
+
+
+BUF_LOGITS, BUF_NEXT_TOKENS, BUF_RESIDUAL, BUF_K_POOL, BUF_V_POOL, BUF_EMBED = range(6)
+
+_hip = None
+
+
+def _hip_memcpy(dst: int, src: int, nbytes: int) -> None:
+    """Synchronous device/host copy through the HIP runtime (hipMemcpyDefault)."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.restype = _i
+        _hip.hipMemcpy.argtypes = [_vp, _vp, _sz, _i]
+    st = _hip.hipMemcpy(dst, src, nbytes, 4)
+    if st != 0:
+        raise LlmkError("hipMemcpy", st, error_string(st))
+
+
+class Engine:
+    """The decode-step engine (``llmk_engine``): a Llama-3 forward pass over batches of token
+    rows, each row one new token of a sequence at a position, with the sequence's block table.
+    It owns the weights (fused layout), the paged K/V pools of every layer, the activations and
+    a GEMM handle. ref: engine/batched.cu:44-120, engine/model.cu:9-33, engine/paged.cu:15-28.
+    """
+
+    def __init__(self, cfg: ModelConfig, max_rows: int, max_pages: int, num_pages: int):
+        self.cfg = cfg
+        self.max_rows, self.max_pages, self.num_pages = max_rows, max_pages, num_pages
+        e = _vp()
+        _check("engine_create", _lib.llmk_engine_create(ctypes.byref(cfg), max_rows, max_pages,
+                                                        num_pages, ctypes.byref(e)))
+        self._e = e
+        self.page_size = 16
+
+    @property
+    def handle(self) -> int:
+        return self._e.value
+
+    def close(self) -> None:
+        if self._e:
+            _lib.llmk_engine_destroy(self._e)
+            self._e = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_weights(self, embed, final_norm, layers) -> None:
+        """Copies the weights in (torch tensors, device or CPU, fp16, contiguous). ``layers`` is a
+        list of dicts keyed by LayerWeights.NAMES, in the reference's [out, in] layout."""
+        fn = "engine_set_weights"
+        c = self.cfg
+        qdim, kvdim, H, I = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim, c.hidden, c.inter
+        shapes = {"attn_norm": (H,), "wq": (qdim, H), "wk": (kvdim, H), "wv": (kvdim, H),
+                  "wo": (H, qdim), "mlp_norm": (H,), "w_gate": (I, H), "w_up": (I, H),
+                  "w_down": (H, I)}
+
+        def ptr(t, shape, name):
+            if tuple(t.shape) != tuple(shape) or t.dtype != torch.float16 or not t.is_contiguous():
+                _fail(fn, f"{name} must be a contiguous float16 tensor of shape {shape}, got "
+                          f"{tuple(t.shape)} {t.dtype}")
+            return t.data_ptr()
+
+        if len(layers) != c.n_layers:
+            _fail(fn, f"{len(layers)} layers given, the model has {c.n_layers}")
+        arr = (LayerWeights * max(1, c.n_layers))()
+        for l, w in enumerate(layers):
+            for name in LayerWeights.NAMES:
+                setattr(arr[l], name, ptr(w[name], shapes[name], f"layers[{l}].{name}"))
+        pe = ptr(embed, (c.vocab, H), "embed")
+        pf = ptr(final_norm, (H,), "final_norm")
+        _check(fn, _lib.llmk_engine_set_weights(self._e, pe, pf, arr))
+
+    def load_weights(self, path: str) -> None:
+        _check("engine_load_weights", _lib.llmk_engine_load_weights(self._e, path.encode()))
+
+    def set_rows(self, tokens, positions, block_tables, logit_rows=None, stream=None) -> None:
+        """Uploads one batch of rows from host arrays (numpy/int sequences): tokens[n],
+        positions[n], block_tables[n, max_pages] (or [n, <= max_pages], zero-padded here), and
+        optionally the rows whose logits are wanted."""
+        import numpy as np
+        tok = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        pos = np.ascontiguousarray(positions, np.int32).reshape(-1)
+        n = tok.size
+        if pos.size != n:
+            _fail("engine_set_rows", "tokens and positions differ in length")
+        tab = np.asarray(block_tables, np.int32).reshape(n, -1)
+        if tab.shape[1] < self.max_pages:
+            tab = np.concatenate([tab, np.zeros((n, self.max_pages - tab.shape[1]), np.int32)], 1)
+        tab = np.ascontiguousarray(tab[:, :self.max_pages])
+        lr = None if logit_rows is None else np.ascontiguousarray(logit_rows, np.int32).reshape(-1)
+        self._rows = (tok, pos, tab, lr)  # keep the host arrays alive until the copy is staged
+        _check("engine_set_rows", _lib.llmk_engine_set_rows(
+            self._e, n, tok.ctypes.data, pos.ctypes.data, tab.ctypes.data,
+            0 if lr is None else lr.size, None if lr is None else lr.ctypes.data,
+            _stream(stream)))
+
+    def forward(self, n_rows: int, n_logit_rows: int = -1, num_splits: int = 0,
+                stream=None) -> None:
+        _check("engine_forward", _lib.llmk_engine_forward(self._e, n_rows, n_logit_rows,
+                                                          num_splits, _stream(stream)))
+
+    def reset_pools(self, stream=None) -> None:
+        _check("engine_reset_pools", _lib.llmk_engine_reset_pools(self._e, _stream(stream)))
+
+    def buffer_ptr(self, which: int, layer: int = 0) -> int:
+        p = _lib.llmk_engine_buffer(self._e, which, layer)
+        if not p:
+            _fail("engine_buffer", f"no buffer {which} for layer {layer}")
+        return p
+
+    def _read(self, which: int, layer: int, shape, dtype) -> torch.Tensor:
+        out = torch.empty(shape, dtype=dtype)
+        nbytes = out.numel() * out.element_size()
+        if nbytes:
+            torch.cuda.synchronize()
+            _hip_memcpy(out.data_ptr(), self.buffer_ptr(which, layer), nbytes)
+        return out
+
+    def logits(self, n: int) -> torch.Tensor:
+        """Host copy of the last forward's logit rows, fp16 [n, vocab]."""
+        return self._read(BUF_LOGITS, 0, (n, self.cfg.vocab), torch.float16)
+
+    def next_tokens(self, n: int) -> torch.Tensor:
+        return self._read(BUF_NEXT_TOKENS, 0, (n,), torch.int32)
+
+    def residual(self, n: int) -> torch.Tensor:
+        return self._read(BUF_RESIDUAL, 0, (n, self.cfg.hidden), torch.float16)
+
+    def pool(self, which: int, layer: int) -> torch.Tensor:
+        """Host copy of one layer's K (BUF_K_POOL) or V (BUF_V_POOL) pool."""
+        c = self.cfg
+        return self._read(which, layer, (self.num_pages, self.page_size, c.n_kv_heads,
+                                         c.head_dim), torch.float16)
+
+    def write_pool(self, which: int, layer: int, src: torch.Tensor) -> None:
+        """Overwrites one layer's pool with a tensor of its size (device or host)."""
+        c = self.cfg
+        n = self.num_pages * self.page_size * c.n_kv_heads * c.head_dim
+        if src.dtype != torch.float16 or src.numel() != n or not src.is_contiguous():
+            _fail("engine_write_pool", f"src must be a contiguous float16 tensor of {n} elements")
+        torch.cuda.synchronize()
+        _hip_memcpy(self.buffer_ptr(which, layer), src.data_ptr(), 2 * n)

@@ -12,6 +12,8 @@ extern "C" const char* llmk_error_string(int status) {
     case LLMK_ERR_SHAPE: return "llmk: size is not a multiple the data layout requires";
     case LLMK_ERR_ALIGNMENT: return "llmk: pointer is not 16-byte aligned";
     case LLMK_ERR_UNSUPPORTED: return "llmk: shape outside what the kernels implement";
+    case LLMK_ERR_BLAS: return "llmk: hipBLASLt could not run the GEMM";
+    case LLMK_ERR_IO: return "llmk: weight file missing, short, or without a required tensor";
     default: return hipGetErrorString(static_cast<hipError_t>(status));
   }
 }

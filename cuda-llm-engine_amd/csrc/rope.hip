@@ -86,12 +86,18 @@ __device__ __forceinline__ u32x4 partner_vec(u32x4 x, bool upper) {
 // partner's 16 bytes with a cross-lane move and writes its own half:
 //   first half:  x1' = x1*c - x2*s        second half: x2' = x2*c + x1*s
 // All loads are issued before the (cos, sin) phase so their latency overlaps it.
-template <int HV, int TASKS, bool FUSED>
+//
+// STRIDED (fused variant only): Q, K and V are read from rows of stride `ld` elements -- the
+// output of one fused QKV projection, q at column 0, k at nh * head_dim, v after k -- and the
+// rotated Q goes to `q`, contiguous [n, nh, head_dim]. The stores are the same as without it.
+template <int HV, int TASKS, bool FUSED, bool STRIDED>
 __global__ void __launch_bounds__(256)
 k_rope_vec(f16* q, const f16* k, const f16* __restrict__ v, f16* k_out, f16* v_pool,
            const int* __restrict__ tables, const int* __restrict__ pos,
            const float* __restrict__ inv_freq, int n_tokens, int nh, int nkv, int tpb,
-           int max_pages, int page_size, FastDiv qdiv, FastDiv kdiv) {
+           int max_pages, int page_size, FastDiv qdiv, FastDiv kdiv, const f16* q_src,
+           int ld) {
+  static_assert(FUSED || !STRIDED, "strided rows come from the fused QKV projection");
   constexpr int HD = 16 * HV, HALF = 8 * HV;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   long long* pool_row = reinterpret_cast<long long*>(smem);       // [tpb] (FUSED only)
@@ -110,10 +116,21 @@ k_rope_vec(f16* q, const f16* k, const f16* __restrict__ v, f16* k_out, f16* v_p
 #pragma unroll
   for (int m = 0; m < TASKS; ++m) {
     const int e = threadIdx.x + m * blockDim.x;
-    if (e < qv) x[m] = ld16_stream(qb + 8 * e);
-    else if (e < qv + kv) x[m] = ld16_stream(kb + 8 * (e - qv));
-    else if (FUSED && e < total) x[m] = ld16_stream(vb + 8 * (e - qv - kv));
-    else x[m] = u32x4{0, 0, 0, 0};
+    if (STRIDED) {
+      // vector e of the concatenated runs -> (token, column) of its strided source row
+      const bool isq = e < qv;
+      const int r = isq ? e : (e < qv + kv ? e - qv : e - qv - kv);
+      const FastDiv dv = isq ? qdiv : kdiv;
+      const int tt = (int)fdiv((uint32_t)r, dv);
+      const int col = r - tt * (int)dv.d;
+      const f16* src = isq ? q_src : (e < qv + kv ? k : v);
+      x[m] = e < total ? ld16_stream(src + (size_t)(t0 + tt) * ld + 8 * col) : u32x4{0, 0, 0, 0};
+    } else {
+      if (e < qv) x[m] = ld16_stream(qb + 8 * e);
+      else if (e < qv + kv) x[m] = ld16_stream(kb + 8 * (e - qv));
+      else if (FUSED && e < total) x[m] = ld16_stream(vb + 8 * (e - qv - kv));
+      else x[m] = u32x4{0, 0, 0, 0};
+    }
   }
   for (int e = threadIdx.x; e < ntok * HALF; e += blockDim.x) {
     const int tt = e / HALF, i = e % HALF;
@@ -198,11 +215,11 @@ static int tokens_per_block(int n_tokens) {
   return tpb;
 }
 
-template <bool FUSED>
+template <bool FUSED, bool STRIDED = false>
 static int rope_vec_launch(f16* q, const f16* k, const f16* v, f16* k_out, f16* v_pool,
                            const int* tables, const int* pos, const float* inv_freq,
                            int n_tokens, int nh, int nkv, int hd, int max_pages, int page_size,
-                           hipStream_t stream) {
+                           hipStream_t stream, const f16* q_src = nullptr, int ld = 0) {
   const int hv = hd / 16;
   const int per_tok = (nh + nkv + (FUSED ? nkv : 0)) * 2 * hv;  // vectors per token
   constexpr int kThreads = 256, kMaxTasks = 16;
@@ -215,8 +232,9 @@ static int rope_vec_launch(f16* q, const f16* k, const f16* v, f16* k_out, f16* 
   const dim3 grid(ceil_div((size_t)n_tokens, (size_t)tpb)), block(kThreads);
   const size_t lds = (FUSED ? 8 * (size_t)tpb : 0) + (size_t)tpb * hd * sizeof(f16);
 #define LLMK_ROPE_LAUNCH(H, TK)                                                                  \
-  return launch(k_rope_vec<H, TK, FUSED>, grid, block, lds, stream, q, k, v, k_out, v_pool,     \
-                tables, pos, inv_freq, n_tokens, nh, nkv, tpb, max_pages, page_size, qdiv, kdiv)
+  return launch(k_rope_vec<H, TK, FUSED, STRIDED>, grid, block, lds, stream, q, k, v, k_out,   \
+                v_pool, tables, pos, inv_freq, n_tokens, nh, nkv, tpb, max_pages, page_size,     \
+                qdiv, kdiv, q_src, ld)
 #define LLMK_ROPE_CASE(H)                \
   case H:                                \
     if (tasks <= 2) LLMK_ROPE_LAUNCH(H, 2);  \
@@ -293,4 +311,29 @@ extern "C" int llmk_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const 
       reinterpret_cast<const f16*>(v), reinterpret_cast<f16*>(k_pool),
       reinterpret_cast<f16*>(v_pool), block_tables, positions, inv_freq, n, n_heads, n_kv_heads,
       head_dim, max_pages, page_size, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int llmk_qkv_rope_scatter(const uint16_t* qkv, int ld, uint16_t* q_out,
+                                     uint16_t* k_pool, uint16_t* v_pool,
+                                     const int32_t* block_tables, const int32_t* positions,
+                                     const float* inv_freq, int n, int max_pages, int page_size,
+                                     int n_heads, int n_kv_heads, int head_dim, void* stream) {
+  if (n < 0 || max_pages <= 0 || page_size <= 0 || n_heads <= 0 || n_kv_heads <= 0 ||
+      head_dim <= 0)
+    return LLMK_ERR_INVALID_VALUE;
+  if (n == 0) return LLMK_OK;
+  if (!qkv || !q_out || !k_pool || !v_pool || !block_tables || !positions || !inv_freq)
+    return LLMK_ERR_INVALID_VALUE;
+  if (!vec_head_dim(head_dim)) return LLMK_ERR_SHAPE;
+  if ((long long)ld < (long long)(n_heads + 2 * n_kv_heads) * head_dim || ld % 8 != 0)
+    return LLMK_ERR_SHAPE;
+  if (!aligned16(qkv) || !aligned16(q_out) || !aligned16(k_pool) || !aligned16(v_pool))
+    return LLMK_ERR_ALIGNMENT;
+  const f16* src = reinterpret_cast<const f16*>(qkv);
+  const f16* k = src + (size_t)n_heads * head_dim;
+  const f16* v = k + (size_t)n_kv_heads * head_dim;
+  return rope_vec_launch<true, true>(
+      reinterpret_cast<f16*>(q_out), k, v, reinterpret_cast<f16*>(k_pool),
+      reinterpret_cast<f16*>(v_pool), block_tables, positions, inv_freq, n, n_heads, n_kv_heads,
+      head_dim, max_pages, page_size, static_cast<hipStream_t>(stream), src, ld);
 }

@@ -134,9 +134,38 @@ k_swiglu_scalar(const f16* __restrict__ gate, const f16* __restrict__ up, f16* _
     out[i] = silu_r16(gate[i]) * up[i];
 }
 
+// Rows of the fused gate/up projection: row r of `gu` holds gate in columns [0, inter) and up
+// in [inter, 2 * inter); out row r = swiglu(gate row, up row). Grid (column blocks, rows), the
+// same per-block body as the flat kernel over each row's two runs.
+template <int UNROLL>
+__global__ void __launch_bounds__(256)
+k_swiglu_rows(const f16* __restrict__ gu, f16* __restrict__ out, int inter) {
+  const size_t r = blockIdx.y;
+  const f16* g = gu + r * 2 * (size_t)inter;
+  const size_t nvec = (size_t)inter / 8;
+  const size_t chunk = (size_t)blockDim.x * UNROLL;
+  const size_t b = (size_t)blockIdx.x * chunk;
+  if (b + chunk <= nvec) swiglu_block<UNROLL>(g, g + inter, out + r * inter, b, nvec, true);
+  else if (b < nvec) swiglu_block<UNROLL>(g, g + inter, out + r * inter, b, nvec, false);
+}
+
 }  // namespace llmk
 
 using namespace llmk;
+
+extern "C" int llmk_swiglu_rows(const uint16_t* gate_up, uint16_t* out, int n_rows, int inter,
+                                void* stream) {
+  if (n_rows < 0 || inter <= 0) return LLMK_ERR_INVALID_VALUE;
+  if (n_rows == 0) return LLMK_OK;
+  if (!gate_up || !out) return LLMK_ERR_INVALID_VALUE;
+  if (inter % 8 != 0) return LLMK_ERR_SHAPE;
+  if (n_rows > 65535) return LLMK_ERR_UNSUPPORTED;
+  if (!aligned16(gate_up) || !aligned16(out)) return LLMK_ERR_ALIGNMENT;
+  constexpr int UNROLL = 2;
+  const dim3 grid(ceil_div((size_t)inter / 8, 256 * UNROLL), (unsigned)n_rows);
+  return launch(k_swiglu_rows<UNROLL>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                reinterpret_cast<const f16*>(gate_up), reinterpret_cast<f16*>(out), inter);
+}
 
 extern "C" int llmk_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n,
                            void* stream) {

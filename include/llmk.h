@@ -41,6 +41,8 @@ extern "C" {
 #define LLMK_ERR_SHAPE 10002         /* size not a multiple the layout requires */
 #define LLMK_ERR_ALIGNMENT 10003     /* a pointer that must be 16-byte aligned is not */
 #define LLMK_ERR_UNSUPPORTED 10004   /* a shape outside what the kernels implement */
+#define LLMK_ERR_BLAS 10005          /* hipBLASLt refused or failed a GEMM */
+#define LLMK_ERR_IO 10006            /* a weight file is missing, short, or lacks a tensor */
 
 /* Human-readable name of a status code (LLMK_ERR_* or hipError_t). Never NULL. */
 LLMK_API const char* llmk_error_string(int status);
@@ -205,6 +207,118 @@ typedef struct llmk_decode_pass {
 } llmk_decode_pass;
 
 LLMK_API int llmk_decode_nongemm_pass(const llmk_decode_pass* pass, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * The decode step around the kernels above: projections (hipBLASLt), the fused layouts they
+ * produce, and an engine that runs a whole Llama-3 forward pass over a batch of token rows.
+ * ------------------------------------------------------------------------------------------ */
+
+/* A GEMM handle: one hipBLASLt handle, a 32 MiB workspace allocated at creation, and a cache
+ * of per-shape plans. Calls on one handle share its workspace, so they must be ordered (one
+ * stream, or one handle per stream), as calls on one cuBLAS handle are. */
+typedef struct llmk_blas llmk_blas;
+LLMK_API int llmk_blas_create(llmk_blas** out);
+LLMK_API void llmk_blas_destroy(llmk_blas* h);
+
+/* y[T, out_features] = x[T, in_features] * W^T, W stored [out_features, in_features] row-major
+ * (a PyTorch Linear without bias); fp16 in and out, fp32 accumulation. The first call of a shape
+ * chooses the algorithm (not during graph capture); later calls only enqueue.
+ * ref: kernels/linear.cuh:5-7, kernels/linear.cu:5-25 (linear; cublasHandle_t -> llmk_blas*). */
+LLMK_API int llmk_linear(llmk_blas* h, const uint16_t* x, const uint16_t* w, uint16_t* y, int T,
+                         int in_features, int out_features, void* stream);
+
+/* RoPE + KV scatter reading the rows of one fused QKV projection: row b of qkv (stride ld
+ * elements) holds q [n_heads, head_dim] at column 0, k [n_kv_heads, head_dim] after it and v
+ * after k. q is rotated into q_out [n, n_heads, head_dim] (contiguous); k is rotated and v copied
+ * into the pools at the llmk_kv_scatter_batch address of positions[b], exactly as
+ * llmk_rope_kv_scatter_batch does with separate q, k, v. head_dim % 16 == 0, ld % 8 == 0,
+ * ld >= (n_heads + 2 n_kv_heads) head_dim; qkv, q_out and the pools 16-byte aligned.
+ * Replaces ref: engine/batched.cu:52-58 (three projections' outputs, rope_apply, two
+ * kv_scatter_batch). New entry point; no single reference function. */
+LLMK_API int llmk_qkv_rope_scatter(const uint16_t* qkv, int ld, uint16_t* q_out,
+                                   uint16_t* k_pool, uint16_t* v_pool,
+                                   const int32_t* block_tables, const int32_t* positions,
+                                   const float* inv_freq, int n, int max_pages, int page_size,
+                                   int n_heads, int n_kv_heads, int head_dim, void* stream);
+
+/* SwiGLU over the rows of one fused gate/up projection: row r of gate_up holds gate in columns
+ * [0, inter) and up in [inter, 2 inter); out[r, j] = llmk_swiglu of (gate[r, j], up[r, j]), out
+ * [n_rows, inter]. inter % 8 == 0, n_rows <= 65535, both pointers 16-byte aligned.
+ * Replaces ref: engine/batched.cu:67-69 (two projections' outputs, swiglu). New entry point. */
+LLMK_API int llmk_swiglu_rows(const uint16_t* gate_up, uint16_t* out, int n_rows, int inter,
+                              void* stream);
+
+/* Model shape and RoPE scaling of a Llama-3 decoder (ref: engine/layer.h:6-9 LayerConfig,
+ * engine/model.h:7 n_layers / vocab, engine/model.cu:20 rope arguments). */
+typedef struct llmk_model_config {
+  int n_layers, hidden, n_heads, n_kv_heads, head_dim, inter, vocab;
+  float eps;
+  double rope_theta, rope_factor, rope_low_freq_factor, rope_high_freq_factor,
+      rope_original_max_pos;
+} llmk_model_config;
+
+/* One layer's weights in the reference's layout: row-major [out, in] projections, [hidden]
+ * norms (ref: engine/layer.h:11-13 LayerWeights). */
+typedef struct llmk_layer_weights {
+  const uint16_t *attn_norm, *wq, *wk, *wv, *wo, *mlp_norm, *w_gate, *w_up, *w_down;
+} llmk_layer_weights;
+
+/* The engine: weights (wq|wk|wv and w_gate|w_up stored concatenated), the paged K and V pools
+ * of every layer ([num_pages, 16, n_kv_heads, head_dim], NaN-filled at creation), row inputs,
+ * activations, the attention workspace and a GEMM handle -- all allocated by create. A row is
+ * one new token of a sequence: (token id, position, block-table row of max_pages page numbers).
+ * Decode is one row per sequence; a prompt is one row per prompt token, all with that
+ * sequence's table. Requires head_dim 64 and n_heads == 4 n_kv_heads (the attention's
+ * preconditions), hidden and inter multiples of 8; page size 16.
+ * ref: engine/model.h:9-19 Model, engine/paged.h:6-13 PagedKVCache, engine/batched.h:13-20
+ * BatchState; engine/model.cu:9-33, engine/paged.cu:15-28, engine/batched.cu:22-35. */
+typedef struct llmk_engine llmk_engine;
+LLMK_API int llmk_engine_create(const llmk_model_config* cfg, int max_rows, int max_pages,
+                                int num_pages, llmk_engine** out);
+LLMK_API void llmk_engine_destroy(llmk_engine* e);
+
+/* Copies the weights (host or device pointers; layers[n_layers]) into the engine. Synchronous. */
+LLMK_API int llmk_engine_set_weights(llmk_engine* e, const uint16_t* embed,
+                                     const uint16_t* final_norm,
+                                     const llmk_layer_weights* layers);
+
+/* Loads dir/weights.bin + dir/index.tsv (Hugging Face tensor names, fp16; the lm head is the
+ * embedding matrix). LLMK_ERR_IO for a missing file or tensor, LLMK_ERR_SHAPE for a tensor
+ * whose shape differs from the config. Synchronous.
+ * ref: engine/model.cu:9-16, engine/layer.cu:12-27, engine/weights.h:9-18, engine/util.h:29-50. */
+LLMK_API int llmk_engine_load_weights(llmk_engine* e, const char* dir);
+
+/* Uploads the rows of the next forward pass from HOST arrays: tokens[n_rows],
+ * positions[n_rows], block_tables[n_rows, max_pages], and the n_logit_rows row indices whose
+ * logits are wanted. Checks every index on the host first (ids < vocab, positions <
+ * max_pages * 16, the table entries of every page a row reads < num_pages, logit rows <
+ * n_rows): LLMK_ERR_INVALID_VALUE and nothing uploaded otherwise. The copy is enqueued on
+ * `stream`; use the same stream for the forward pass. Not capturable (it waits for the
+ * previous upload to leave the staging buffer). ref: engine/batched.cu:87-105. */
+LLMK_API int llmk_engine_set_rows(llmk_engine* e, int n_rows, const int32_t* tokens,
+                                  const int32_t* positions, const int32_t* block_tables,
+                                  int n_logit_rows, const int32_t* logit_rows, void* stream);
+
+/* Enqueues the forward pass over the first n_rows uploaded rows: embedding, every layer (K and
+ * V of each row written to the pools), final norm, logits [nl, vocab] and their argmax [nl]
+ * (nl = n_rows if n_logit_rows < 0, else the uploaded logit rows). num_splits <= 0 picks the
+ * split count (capped at 32, the workspace). Allocates nothing; capturable into a HIP graph
+ * for a fixed n_rows. ref: engine/batched.cu:107-120 (decode_step_gpu), :44-72
+ * (layer_forward_batched), :150 (argmax_rows in model_decode_batch_greedy). */
+LLMK_API int llmk_engine_forward(llmk_engine* e, int n_rows, int n_logit_rows, int num_splits,
+                                 void* stream);
+
+/* Device buffers of the engine, for reading results and for tests. */
+#define LLMK_BUF_LOGITS 0      /* fp16 [max_rows, vocab]: the last forward's logit rows */
+#define LLMK_BUF_NEXT_TOKENS 1 /* int32 [max_rows]: their argmax */
+#define LLMK_BUF_RESIDUAL 2    /* fp16 [max_rows, hidden]: the residual stream after the pass */
+#define LLMK_BUF_K_POOL 3      /* fp16 [num_pages, 16, n_kv_heads, head_dim] of `layer` */
+#define LLMK_BUF_V_POOL 4      /* same, V */
+#define LLMK_BUF_EMBED 5       /* fp16 [vocab, hidden]: the embedding (and lm head) matrix */
+LLMK_API void* llmk_engine_buffer(llmk_engine* e, int which, int layer);
+
+/* Refills every pool slot with 0x7F7F (fp16 NaN), as at creation. Not capturable. */
+LLMK_API int llmk_engine_reset_pools(llmk_engine* e, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -18,6 +18,9 @@
  *   or_swiglu                torch silu * up fixture; g = 0 -> 0; large |g| limits
  *   or_kv_scatter(_batch)    numpy scatter by the closed-form row address; untouched rows keep
  *                            their 0x7F7F poison; exactly T (or n) rows change
+ *   or_linear                float64 matmul of the same fp16 inputs (error within the fp32
+ *                            summation bound); identity and one-hot weights select exact
+ *                            columns; torch.nn.functional.linear on the CPU in float32
  */
 #define _GNU_SOURCE
 #include "oracle.h"
@@ -313,6 +316,35 @@ void or_argmax_rows(const uint16_t* logits, int32_t* out, int n_rows, int n_cols
 }
 
 /* ------------------------------------------------------------------------------------------ */
+/* projection                                                                                   */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Output features [o0, o1) of y = x W^T for every row t: the fp32 sum of fp32 products in index
+ * order, rounded once to fp16. */
+static void linear_cols(const uint16_t* x, const uint16_t* w, uint16_t* y, int T, int in, int out,
+                        size_t o0, size_t o1) {
+  float* xf = (float*)malloc(sizeof(float) * (size_t)in * (size_t)T);
+  float* wf = (float*)malloc(sizeof(float) * (size_t)in);
+  or_h2f_array(x, xf, (size_t)in * (size_t)T);
+  for (size_t o = o0; o < o1; ++o) {
+    or_h2f_array(w + o * (size_t)in, wf, (size_t)in);
+    for (int t = 0; t < T; ++t) {
+      const float* xr = xf + (size_t)t * in;
+      float acc = 0.0f;
+      for (int k = 0; k < in; ++k) acc += xr[k] * wf[k];
+      y[(size_t)t * out + o] = or_f2h(acc);
+    }
+  }
+  free(xf);
+  free(wf);
+}
+
+void or_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int T, int in_features,
+               int out_features) {
+  linear_cols(x, w, y, T, in_features, out_features, 0, (size_t)out_features);
+}
+
+/* ------------------------------------------------------------------------------------------ */
 /* row-parallel variants (CPU baseline)                                                         */
 /* ------------------------------------------------------------------------------------------ */
 
@@ -343,6 +375,9 @@ static void* run_job(void* p) {
     case 3:
       or_embedding_lookup(j->i0, j->ids + j->r0, j->o0 + j->r0 * (size_t)j->a,
                           (int)(j->r1 - j->r0), j->a);
+      break;
+    case 4:
+      linear_cols(j->i0, j->i1, j->o0, j->a, j->b, j->c, j->r0, j->r1);
       break;
   }
   return NULL;
@@ -482,3 +517,16 @@ long long or_f16c_mismatches(int nthreads) {
   return -1;
 }
 #endif
+
+void or_linear_mt(const uint16_t* x, const uint16_t* w, uint16_t* y, int T, int in_features,
+                  int out_features, int nthreads) {
+  job_t j = {0};
+  j.kind = 4;
+  j.i0 = x;
+  j.i1 = w;
+  j.o0 = y;
+  j.a = T;
+  j.b = in_features;
+  j.c = out_features;
+  run_split(j, (size_t)out_features, nthreads);
+}

@@ -82,6 +82,17 @@ void or_attention_decode_paged(const uint16_t* q, const uint16_t* k_pool, const 
  * value above -inf gives INT_MAX (the reduction's initial index). */
 void or_argmax_rows(const uint16_t* logits, int32_t* out, int n_rows, int n_cols);
 
+/* Projection y[T, out] = x[T, in] W^T with W [out, in] row-major, fp16 in and out: each output
+ * is the fp32 sum, in index order, of the fp32 products float(x) * float(w), rounded once to
+ * fp16 -- a GEMM with fp16 data and fp32 accumulation, as ref: kernels/linear.cu:8-20 requests
+ * of cuBLAS (CUBLAS_COMPUTE_32F). The summation order of a library GEMM is unspecified, so the
+ * GPU agrees within tolerance, not bit for bit. or_linear_mt splits the output features over
+ * nthreads threads (same results). */
+void or_linear(const uint16_t* x, const uint16_t* w, uint16_t* y, int T, int in_features,
+               int out_features);
+void or_linear_mt(const uint16_t* x, const uint16_t* w, uint16_t* y, int T, int in_features,
+                  int out_features, int nthreads);
+
 /* Row-parallel variants for the CPU baseline: the same per-row code split over nthreads
  * threads by contiguous row ranges (results identical to the single-thread functions). */
 void or_add_rmsnorm_mt(uint16_t* residual, const uint16_t* x, const uint16_t* w, uint16_t* out,

@@ -114,3 +114,44 @@ def attention_f64(case: dict) -> np.ndarray:
             p = np.exp(s - s.max())
             out[b, h] = (p / p.sum()) @ V[:, g, :]
     return out
+
+
+# A small Llama-3 shape for whole-model checks: the engine's constraints (head_dim 64, 4 query
+# heads per kv head, page size 16) at a size the scalar oracle runs in well under a second.
+TINY = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=1, head_dim=64, inter=512, vocab=512,
+            eps=1e-5, rope_theta=500000.0, rope_factor=32.0, rope_low_freq_factor=1.0,
+            rope_high_freq_factor=4.0, rope_original_max_pos=8192.0)
+
+
+def tiny_weights(seed: int, embed_std: float = 0.02, cfg: dict = TINY) -> dict:
+    """Seeded fp16 weights under the Hugging Face names: projections ~N(0, 0.05), the
+    embedding ~N(0, embed_std), norm weights ~N(1, 0.1)."""
+    rng = np.random.default_rng(seed)
+    c = cfg
+    H, I, V = c["hidden"], c["inter"], c["vocab"]
+    qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+
+    def f16(shape, scale):
+        return (scale * rng.standard_normal(shape, dtype=np.float32)).astype(np.float16)
+
+    w = {"model.embed_tokens.weight": f16((V, H), embed_std),
+         "model.norm.weight": (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)}
+    for l in range(c["n_layers"]):
+        p = f"model.layers.{l}."
+        w[p + "input_layernorm.weight"] = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+        w[p + "post_attention_layernorm.weight"] = (1 + 0.1 * rng.standard_normal(H)).astype(
+            np.float16)
+        for name, shape in (("self_attn.q_proj", (qd, H)), ("self_attn.k_proj", (kvd, H)),
+                            ("self_attn.v_proj", (kvd, H)), ("self_attn.o_proj", (H, qd)),
+                            ("mlp.gate_proj", (I, H)), ("mlp.up_proj", (I, H)),
+                            ("mlp.down_proj", (H, I))):
+            w[p + name + ".weight"] = f16(shape, 0.05)
+    return w
+
+
+def oracle_pools(num_pages: int, cfg: dict = TINY):
+    """Per-layer K and V pools for the oracle, every slot 0x7F7F (ref: engine/paged.cu:22)."""
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    n = num_pages * 16 * kvd
+    return ([np.full(n, POISON, np.uint16) for _ in range(cfg["n_layers"])],
+            [np.full(n, POISON, np.uint16) for _ in range(cfg["n_layers"])])

@@ -1,0 +1,334 @@
+"""GPU parity of the decode-step pieces and the engine against the CPU oracle.
+
+- llmk_linear (hipBLASLt) vs the oracle's projection, with the reference's projection test rule
+  |d| <= 3e-3 + 8e-3 |e| (ref: tests/test_linear.cu:47) at the engine's shapes.
+- llmk_qkv_rope_scatter and llmk_swiglu_rows (the fused layouts) vs the oracle's separate
+  operations on the same data: bit-exact, like the unfused kernels.
+- The engine (llmk_engine_*) vs oracle.engine_forward on a small Llama-3 shape and on the
+  Llama-3.2-1B shape: mixed prefill and decode rows, shuffled pages, teacher-forced steps.
+  Library GEMMs sum in their own order, so the bar is the reference's for its engine against
+  Hugging Face: relative L2 of every logit row below 5e-3 (ref:
+  tests/test_generate_batched.cu:53), the same greedy token wherever the oracle's top two are
+  clearly apart, and the same set of written pool slots with every other slot still 0x7F7F.
+- The engine's forward pass captured in a HIP graph replays bit-identically to eager runs.
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import POISON, TINY, normal_f16, oracle_pools, tiny_weights
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def dev(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.float16)).to(DEV)
+
+
+def dev_i32(a) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(DEV)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def linear_rule(got: np.ndarray, exp: np.ndarray):
+    g = got.view(np.float16).astype(np.float64)
+    e = exp.view(np.float16).astype(np.float64)
+    bad = ~(np.abs(g - e) <= 3e-3 + 8e-3 * np.abs(e))
+    return int(bad.sum()), float(np.mean(got == exp))
+
+
+# ------------------------------------------------------------------------------------------
+# projections
+# ------------------------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def blas(llmk):
+    return llmk.Blas()
+
+
+@pytest.mark.parametrize("T,K,N", [(1, 2048, 3072), (8, 2048, 16384), (37, 8192, 2048),
+                                   (256, 512, 1024), (402, 2048, 2048), (3, 256, 512)])
+def test_linear_matches_oracle(llmk, orc, blas, T, K, N):
+    rng = np.random.default_rng(0x5EED0200 + T)
+    x = normal_f16(rng, (T, K))
+    w = normal_f16(rng, (N, K), std=0.02)
+    y = torch.full((T * N + 64,), float("nan"), dtype=torch.float16, device=DEV)
+    print(f"linear T={T} K={K} N={N}", flush=True)
+    llmk.linear(blas, dev(x), dev(w), y, T, K, N)
+    torch.cuda.synchronize()
+    got = host(y)
+    assert np.all(got[T * N:] == 0x7E00), "write past the output"
+    bad, exact = linear_rule(got[:T * N], orc.linear(x, w, T, K, N, threads=16).ravel())
+    print(f"  bad {bad} exact {100 * exact:.2f}%")
+    assert bad == 0 and exact > 0.9
+
+
+def test_linear_rejects_bad_arguments(llmk, blas):
+    x = torch.zeros(4, 64, dtype=torch.float16, device=DEV)
+    with pytest.raises(llmk.LlmkError):
+        llmk.linear(blas, x, x, x, 8, 64, 64)          # x holds fewer than T * in values
+    st = llmk.lib().llmk_linear(blas.handle, x.data_ptr(), x.data_ptr(), x.data_ptr(), 4, 0, 4,
+                                None)
+    assert st == llmk.LLMK_ERR_INVALID_VALUE
+    assert llmk.lib().llmk_linear(blas.handle, 0, 0, 0, 0, 64, 64, None) == llmk.LLMK_OK
+
+
+# ------------------------------------------------------------------------------------------
+# fused layouts
+# ------------------------------------------------------------------------------------------
+def test_qkv_rope_scatter_matches_the_separate_operations(llmk, orc):
+    rng = np.random.default_rng(0x5EED0210)
+    n, nh, nkv, hd, ps, max_pages = 37, 32, 8, 64, 16, 6
+    qdim, kvdim = nh * hd, nkv * hd
+    ld = qdim + 2 * kvdim + 8  # a padded row stride
+    num_pages = n * max_pages
+    qkv = normal_f16(rng, (n, ld))
+    pos = rng.integers(0, max_pages * ps, n).astype(np.int32)
+    tables = rng.permutation(num_pages).astype(np.int32).reshape(n, max_pages)  # distinct slots
+    inv = orc.compute_rope_inv_freq(hd, 500000.0, 32.0, 1.0, 4.0, 8192.0)
+    q = np.ascontiguousarray(qkv[:, :qdim])
+    k = np.ascontiguousarray(qkv[:, qdim:qdim + kvdim])
+    v = np.ascontiguousarray(qkv[:, qdim + kvdim:qdim + 2 * kvdim])
+    kp = np.full(num_pages * ps * kvdim, POISON, np.uint16)
+    vp = kp.copy()
+    q_exp = q.copy()
+    orc.rope_kv_scatter_batch(q_exp, k, v, kp, vp, tables, pos, inv, n, max_pages, ps, nh, nkv,
+                              hd)
+    d_kp, d_vp = dev(np.full_like(kp, POISON)), dev(np.full_like(vp, POISON))
+    q_out = torch.full((n * qdim,), float("nan"), dtype=torch.float16, device=DEV)
+    d_inv = torch.from_numpy(inv).to(DEV)
+    llmk.qkv_rope_scatter(dev(qkv), ld, q_out, d_kp, d_vp, dev_i32(tables), dev_i32(pos), d_inv,
+                          n, max_pages, ps, nh, nkv, hd)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q_out), q_exp.ravel())
+    assert np.array_equal(host(d_kp), kp)
+    assert np.array_equal(host(d_vp), vp)
+    # and the same bits as the unfused GPU entry point on the split buffers
+    q2, kp2, vp2 = dev(q), dev(np.full_like(kp, POISON)), dev(np.full_like(vp, POISON))
+    llmk.rope_kv_scatter_batch(q2, dev(k), dev(v), kp2, vp2, dev_i32(tables), dev_i32(pos),
+                               d_inv, n, max_pages, ps, nh, nkv, hd)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q2).ravel(), host(q_out))
+    assert np.array_equal(host(kp2), kp) and np.array_equal(host(vp2), vp)
+
+
+@pytest.mark.parametrize("n,inter", [(19, 8192), (5, 520), (1, 8)])
+def test_swiglu_rows_matches_oracle(llmk, orc, n, inter):
+    rng = np.random.default_rng(0x5EED0220 + inter)
+    gu = normal_f16(rng, (n, 2 * inter))
+    gu[0, :8] = np.array([0.0, -0.0, 20.0, -20.0, 88.0, -88.0, 6e-8, -6e-8],
+                         np.float16).view(np.uint16)
+    exp = orc.swiglu(np.ascontiguousarray(gu[:, :inter]), np.ascontiguousarray(gu[:, inter:]))
+    out = torch.full((n * inter + 8,), float("nan"), dtype=torch.float16, device=DEV)
+    llmk.swiglu_rows(dev(gu), out, n, inter)
+    torch.cuda.synchronize()
+    got = host(out)
+    assert np.array_equal(got[:n * inter], exp.ravel())
+    assert np.all(got[n * inter:] == 0x7E00), "write past the output"
+
+
+# ------------------------------------------------------------------------------------------
+# the engine
+# ------------------------------------------------------------------------------------------
+def make_engine(llmk, cfg: dict, w: dict, max_rows: int, max_pages: int, num_pages: int):
+    weights = importlib.import_module("llmk.weights")
+    e = llmk.Engine(llmk.ModelConfig(**cfg), max_rows, max_pages, num_pages)
+    tensors = {k: torch.from_numpy(np.ascontiguousarray(v)).to(DEV) if isinstance(v, np.ndarray)
+               else v for k, v in w.items()}
+    e.set_weights(*weights.engine_layers(tensors, cfg))
+    return e
+
+
+class Session:
+    """Sequences with shuffled pages; builds the rows of a step (prefill chunks and decode
+    tokens) and runs them through both the engine and the oracle, teacher-forcing both with the
+    oracle's greedy tokens."""
+
+    def __init__(self, llmk, orc, cfg, w_engine, w_oracle, n_seqs, max_rows, max_pages,
+                 num_pages, seed):
+        self.cfg, self.orc = cfg, orc
+        self.w = {k: np.asarray(v).view(np.uint16) for k, v in w_oracle.items()}
+        self.rng = np.random.default_rng(seed)
+        self.max_pages, self.num_pages = max_pages, num_pages
+        perm = self.rng.permutation(num_pages).astype(np.int32)
+        assert n_seqs * max_pages <= num_pages
+        self.tables = perm[:n_seqs * max_pages].reshape(n_seqs, max_pages)
+        self.len = np.zeros(n_seqs, np.int64)
+        self.engine = make_engine(llmk, cfg, w_engine, max_rows, max_pages, num_pages)
+        self.kp, self.vp = oracle_pools(num_pages, cfg)
+        self.last = {}
+
+    def step(self, parts):
+        """parts: list of (seq, tokens or None); None = one decode row fed with the sequence's
+        last greedy token. Returns (engine logits, oracle logits, oracle next) of the last row of
+        every part."""
+        tok, pos, tab, logit_rows = [], [], [], []
+        for s, toks in parts:
+            toks = [self.last[s]] if toks is None else list(toks)
+            for t in toks:
+                tok.append(t)
+                pos.append(self.len[s])
+                tab.append(self.tables[s])
+                self.len[s] += 1
+            logit_rows.append(len(tok) - 1)
+        tok, pos, tab = np.array(tok, np.int32), np.array(pos, np.int32), np.array(tab, np.int32)
+        e = self.engine
+        e.set_rows(tok, pos, tab, logit_rows)
+        e.forward(len(tok), len(logit_rows))
+        torch.cuda.synchronize()
+        got = e.logits(len(logit_rows)).numpy().view(np.uint16)
+        got_next = e.next_tokens(len(logit_rows)).numpy()
+        exp, exp_next, _ = self.orc.engine_forward(self.cfg, self.w, tok, pos, tab, self.kp,
+                                                   self.vp, logit_rows, threads=16)
+        for (s, _), t in zip(parts, exp_next):
+            self.last[s] = int(t)
+        return got, got_next, exp, exp_next
+
+    def check_pools(self, llmk):
+        written_e, written_o = [], []
+        for l in range(self.cfg["n_layers"]):
+            for which, pools in ((llmk.BUF_K_POOL, self.kp), (llmk.BUF_V_POOL, self.vp)):
+                g = self.engine.pool(which, l).numpy().view(np.uint16).reshape(-1, 16, self.cfg[
+                    "n_kv_heads"] * self.cfg["head_dim"])
+                o = pools[l].reshape(g.shape)
+                we, wo = (g != POISON).any(2), (o != POISON).any(2)
+                assert np.array_equal(we, wo), "different pool slots written"
+                assert np.all(g[~we] == POISON)
+                a = g[we].view(np.float16).astype(np.float64)
+                b = o[wo].view(np.float16).astype(np.float64)
+                rel = np.linalg.norm(a - b) / np.linalg.norm(b)
+                assert rel < 5e-3, (l, which, rel)
+                written_e.append(int(we.sum()))
+        return written_e
+
+
+def check_logits(orc, got, got_next, exp, exp_next, what):
+    g = got.view(np.float16).astype(np.float64)
+    e = exp.view(np.float16).astype(np.float64)
+    rel = np.linalg.norm(g - e, axis=1) / np.linalg.norm(e, axis=1)
+    top2 = np.sort(e, axis=1)[:, -2:]
+    clear = top2[:, 1] - top2[:, 0] > 0.05 * np.abs(top2[:, 1]).clip(1, None)
+    print(f"{what}: rel L2 max {rel.max():.2e} exact {100 * np.mean(got == exp):.1f}% "
+          f"clear {clear.sum()}/{len(clear)}", flush=True)
+    assert rel.max() < 5e-3, rel
+    assert np.array_equal(got_next[clear], exp_next[clear])
+    # the engine's own argmax is exactly the argmax of its logits
+    assert np.array_equal(got_next, orc.argmax_rows(got, got.shape[0], got.shape[1]))
+
+
+def test_engine_matches_oracle_small_model(llmk, orc):
+    w = tiny_weights(0x5EED0230, embed_std=0.5)
+    rng = np.random.default_rng(0x5EED0231)
+    s = Session(llmk, orc, TINY, w, w, n_seqs=3, max_rows=64, max_pages=8, num_pages=30,
+                seed=0x5EED0232)
+    V = TINY["vocab"]
+    prompts = [rng.integers(0, V, L) for L in (20, 33, 7)]
+    # step 1: two prompts in one batch (53 rows); step 2: the third prompt plus two decode rows;
+    # then decode steps for all three
+    plan = [[(0, prompts[0]), (1, prompts[1])], [(2, prompts[2]), (0, None), (1, None)]]
+    plan += [[(0, None), (1, None), (2, None)] for _ in range(5)]
+    for i, parts in enumerate(plan):
+        check_logits(orc, *s.step(parts), f"step {i}")
+    written = s.check_pools(llmk)
+    assert written[0] == int(s.len.sum())  # one slot per row ever run
+
+
+def test_engine_graph_replays_match_eager(llmk, orc):
+    w = tiny_weights(0x5EED0240, embed_std=0.5)
+    e = make_engine(llmk, TINY, w, 16, 4, 64)
+    rng = np.random.default_rng(0x5EED0241)
+    n = 12  # two prompts, of 5 and 7 tokens, in one batch of rows
+    tok = rng.integers(0, TINY["vocab"], n).astype(np.int32)
+    pos = np.array(list(range(5)) + list(range(7)), np.int32)
+    pages = rng.permutation(64).astype(np.int32).reshape(16, 4)
+    tab = np.array([pages[0]] * 5 + [pages[1]] * 7, np.int32)
+    e.set_rows(tok, pos, tab)
+    e.forward(n)                      # eager: chooses the GEMM plans before capture
+    torch.cuda.synchronize()
+    ref_logits = e.logits(n).view(torch.int16).clone()
+    ref_pool = e.pool(llmk.BUF_K_POOL, 1).view(torch.int16).clone()
+    assert not torch.isnan(ref_logits.view(torch.float16)).any()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        e.forward(n, stream=s)        # warm on the capture stream too
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        e.forward(n)
+    junk = torch.randn(1 << 20, device=DEV)
+    for r in range(4):
+        e.reset_pools()
+        torch.cuda.synchronize()
+        junk.mul_(1.0001)             # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(e.logits(n).view(torch.int16), ref_logits), f"replay {r}"
+        assert torch.equal(e.pool(llmk.BUF_K_POOL, 1).view(torch.int16), ref_pool), f"replay {r}"
+
+
+def test_engine_loads_the_reference_weight_format(llmk, tmp_path):
+    weights = importlib.import_module("llmk.weights")
+    w = tiny_weights(0x5EED0250, embed_std=0.5)
+    weights.write_weights_dir(str(tmp_path), w)
+    a = make_engine(llmk, TINY, w, 8, 2, 16)
+    b = llmk.Engine(llmk.ModelConfig(**TINY), 8, 2, 16)
+    b.load_weights(str(tmp_path))
+    tok = np.arange(8, dtype=np.int32) * 7
+    pos = np.arange(8, dtype=np.int32)
+    tab = np.tile(np.array([[3, 5]], np.int32), (8, 1))
+    for e in (a, b):
+        e.set_rows(tok, pos, tab)
+        e.forward(8)
+    torch.cuda.synchronize()
+    assert torch.equal(a.logits(8), b.logits(8))
+    # a missing directory, and a config whose shapes the files do not have
+    with pytest.raises(llmk.LlmkError) as ei:
+        b.load_weights(str(tmp_path / "nowhere"))
+    assert ei.value.status == llmk.LLMK_ERR_IO
+    c = llmk.Engine(llmk.ModelConfig(**dict(TINY, vocab=TINY["vocab"] + 8)), 8, 2, 16)
+    with pytest.raises(llmk.LlmkError) as ei:
+        c.load_weights(str(tmp_path))
+    assert ei.value.status == llmk.LLMK_ERR_SHAPE
+
+
+def test_engine_rejects_rows_that_address_outside_its_buffers(llmk):
+    e = make_engine(llmk, TINY, tiny_weights(0x5EED0260), 4, 2, 8)
+    ok = dict(tokens=[1, 2], positions=[0, 17], block_tables=[[0, 1], [2, 3]])
+    e.set_rows(**ok)
+    bad = [dict(ok, tokens=[1, TINY["vocab"]]), dict(ok, tokens=[-1, 2]),
+           dict(ok, positions=[0, 32]), dict(ok, positions=[-1, 0]),
+           dict(ok, block_tables=[[0, 1], [2, 8]]), dict(ok, block_tables=[[-1, 1], [2, 3]])]
+    for b in bad:
+        with pytest.raises(llmk.LlmkError):
+            e.set_rows(**b)
+    with pytest.raises(llmk.LlmkError):
+        e.set_rows(**ok, logit_rows=[2])
+    with pytest.raises(llmk.LlmkError):
+        e.forward(5)                                   # more rows than max_rows
+    with pytest.raises(llmk.LlmkError) as ei:
+        llmk.Engine(llmk.ModelConfig(**dict(TINY, head_dim=128)), 4, 2, 8)
+    assert ei.value.status == llmk.LLMK_ERR_SHAPE
+
+
+def test_engine_matches_oracle_llama_3_2_1b_shape(llmk, orc):
+    """The Llama-3.2-1B shape (16 layers, vocab 128256) with seeded random weights: two prompts
+    and one decode step."""
+    weights = importlib.import_module("llmk.weights")
+    cfg = llmk.ModelConfig().as_dict()
+    w_dev = weights.random_weights(cfg, 0x5EED0270, device=DEV, std=0.02, embed_std=0.5)
+    w_host = {k: v.cpu().numpy() for k, v in w_dev.items()}
+    s = Session(llmk, orc, cfg, w_dev, w_host, n_seqs=2, max_rows=16, max_pages=4,
+                num_pages=12, seed=0x5EED0271)
+    del w_dev
+    rng = np.random.default_rng(0x5EED0272)
+    check_logits(orc, *s.step([(0, rng.integers(0, cfg["vocab"], 5)),
+                               (1, rng.integers(0, cfg["vocab"], 9))]), "1B prefill")
+    check_logits(orc, *s.step([(0, None), (1, None)]), "1B decode")
+    s.check_pools(llmk)
