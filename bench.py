@@ -48,7 +48,9 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--kernels", choices=["all", "headline"], default="all")
+    ap.add_argument("--kernels", choices=["all", "headline", "step"], default="all",
+                    help="all: every configuration; headline: config 2 only; step: config 2 and "
+                         "the engine's decode step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
@@ -318,6 +320,9 @@ def main() -> int:
     del sets
     torch.cuda.empty_cache()
 
+    if args.kernels == "step":
+        kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W))
+
     if args.kernels == "all":
         # config 1: RMSNorm [16, 2048] (the reference's CPU-plumbing case, on the GPU)
         sets1 = [wl.add_rmsnorm_inputs(16, hidden, seed=wl.SEED_BASE + 1 + 100 * i)
@@ -440,6 +445,12 @@ def main() -> int:
         del logits
         torch.cuda.empty_cache()
 
+        # the whole decode step of the engine (Llama-3.2-1B shape, seeded random weights):
+        # 256 sequences with context lengths uniform in [1, 2048] (the attention workload), one
+        # new token each, every layer's K/V pool pre-filled for the cached positions; one HIP
+        # graph per step (ref: engine/batched.cu:81-120, model_decode_batch_greedy :146-150)
+        kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W))
+
         # copy probe: practical HBM ceiling (ref: bench/bandwidth.cu)
         nb = 1 << 30
         bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(4)]
@@ -471,6 +482,54 @@ def main() -> int:
     }
     print(json.dumps(rec), flush=True)
     return 0
+
+
+def bench_decode_step(llmk, wl, timer, torch, np, dev, K, W) -> dict:
+    import importlib
+    weights = importlib.import_module("llmk.weights")
+    cfg = llmk.ModelConfig()
+    lens = wl.attention_lens()
+    tokens, pos, tables, used = wl.decode_step_rows(lens)
+    n = lens.size
+    eng = llmk.Engine(cfg, max_rows=n, max_pages=128, num_pages=used)
+    w = weights.random_weights(cfg, wl.SEED_BASE + 9, device=dev)
+    eng.set_weights(*weights.engine_layers(w, cfg))
+    del w
+    g = torch.Generator(device=dev)
+    g.manual_seed(wl.SEED_BASE + 10)
+    fill = torch.randn(used * wl.PAGE * wl.N_KV * wl.HEAD_DIM, generator=g, device=dev).half()
+    for l in range(cfg.n_layers):
+        for which in (llmk.BUF_K_POOL, llmk.BUF_V_POOL):
+            eng.write_pool(which, l, fill)
+    del fill
+    torch.cuda.empty_cache()
+    eng.set_rows(tokens, pos, tables)
+    eng.forward(n)  # eager once: chooses the GEMM plans
+    torch.cuda.synchronize()
+    if not torch.isfinite(eng.logits(n).float()).all():
+        raise RuntimeError("decode step produced non-finite logits")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        eng.forward(n, stream=s)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eng.forward(n)
+    steps = max(20, K // 4)
+    t = timer.run(lambda i: graph.replay(), 1, steps, max(5, W // 4))
+    nbytes = wl.bytes_decode_step(lens)
+    e = kernel_entry("decode step 1B, 256 seqs (graph)", nbytes, t, None, {
+        "tokens_per_s": round(n / t["mean_s"], 1), "seqs": int(n),
+        "context_tokens": int(lens.sum()), "layers": cfg.n_layers,
+        "note": "engine forward pass: hipBLASLt projections + libllmk kernels, one HIP graph; "
+                "bytes = sum of the step's kernels' algorithmic bytes (weights 2.47 GB, KV "
+                "cache reads, activations between kernels)"})
+    log(f"    -> {e['tokens_per_s']:.0f} tokens/s")
+    eng.close()
+    del graph
+    torch.cuda.empty_cache()
+    return {"decode_step_1b_256": e}
 
 
 def cpu_baseline(inp, rows, hidden, nbytes, seconds, eps):

@@ -7,9 +7,15 @@
 // y = op_T(W) * x -- the same formulation as the reference's cuBLAS call.
 //
 // A handle owns one hipBLASLt handle, a 32 MiB workspace allocated once at creation, and a
-// cache of per-shape plans (descriptors, layouts, and the heuristic's first algorithm). The
-// heuristic query runs on the first call of a shape only; later calls, including calls made
-// while a stream is being captured into a HIP graph, only enqueue the GEMM.
+// cache of per-shape plans (descriptors, layouts and the chosen algorithm). The plan is made on
+// the first call of a shape: up to kCandidates algorithms from hipBLASLt's heuristic are each
+// timed on the caller's stream with the caller's operands (y is overwritten, then computed
+// again by the real call), and the fastest is kept. Each timed run follows a 512 MiB write that
+// evicts the 256 MB Infinity Cache, because in a decode step every weight matrix arrives cold
+// from HBM (2.5 GB of weights stream through per step); with warm caches the ranking favours
+// small tiles that lose on cold data. The flush buffer lives only while a plan is made. When
+// the stream is being captured into a HIP graph the first candidate is taken untimed; later
+// calls only enqueue the GEMM.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -22,6 +28,9 @@
 namespace {
 
 constexpr size_t kWorkspaceBytes = 32u << 20;
+constexpr int kCandidates = 128;  // heuristic results considered per shape
+constexpr int kTimedRuns = 3;     // timed cold launches per candidate (after one untimed)
+constexpr size_t kFlushBytes = 512u << 20;
 
 struct Plan {
   hipblasLtMatmulDesc_t desc = nullptr;
@@ -50,8 +59,37 @@ struct llmk_blas {
 
 namespace {
 
-// Builds the plan of one (T, in, out) shape. Returns LLMK_OK or LLMK_ERR_BLAS.
-int make_plan(llmk_blas* h, int T, int in, int out, Plan* p) {
+// Smallest duration of kTimedRuns cold launches of one algorithm (each after a write of the
+// flush buffer, when there is one), or a negative value if it fails to run.
+float time_algo(llmk_blas* h, const Plan& q, const hipblasLtMatmulAlgo_t& algo, size_t ws,
+                const void* x, const void* w, void* y, void* flush, hipStream_t stream) {
+  const float alpha = 1.0f, beta = 0.0f;
+  auto run = [&] {
+    return hipblasLtMatmul(h->lt, q.desc, &alpha, w, q.a, x, q.b, &beta, y, q.d, y, q.d, &algo,
+                           h->workspace, ws, stream) == HIPBLAS_STATUS_SUCCESS;
+  };
+  if (!run()) return -1.0f;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0f;
+  float best = -1.0f;
+  bool ok = true;
+  for (int i = 0; ok && i < kTimedRuns; ++i) {
+    if (flush) ok = hipMemsetAsync(flush, i & 0xFF, kFlushBytes, stream) == hipSuccess;
+    ok = ok && hipEventRecord(e0, stream) == hipSuccess && run() &&
+         hipEventRecord(e1, stream) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+    float ms = 0.0f;
+    ok = ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+    if (ok && (best < 0.0f || ms < best)) best = ms;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return ok ? best : -1.0f;
+}
+
+// Builds the plan of one (T, in, out) shape, timing the candidates on `stream` with the call's
+// operands unless the stream is capturing. Returns LLMK_OK or LLMK_ERR_BLAS.
+int make_plan(llmk_blas* h, int T, int in, int out, const void* x, const void* w, void* y,
+              hipStream_t stream, Plan* p) {
   Plan q;
   const hipblasOperation_t opA = HIPBLAS_OP_T, opB = HIPBLAS_OP_N;
   bool ok = hipblasLtMatmulDescCreate(&q.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) ==
@@ -71,15 +109,32 @@ int make_plan(llmk_blas* h, int T, int in, int out, Plan* p) {
                                                &ws, sizeof(ws)) == HIPBLAS_STATUS_SUCCESS;
   }
   if (ok) {
-    hipblasLtMatmulHeuristicResult_t res[8];
+    hipblasLtMatmulHeuristicResult_t res[kCandidates];
     int found = 0;
-    ok = hipblasLtMatmulAlgoGetHeuristic(h->lt, q.desc, q.a, q.b, q.d, q.d, pref, 8, res,
-                                         &found) == HIPBLAS_STATUS_SUCCESS;
+    ok = hipblasLtMatmulAlgoGetHeuristic(h->lt, q.desc, q.a, q.b, q.d, q.d, pref, kCandidates,
+                                         res, &found) == HIPBLAS_STATUS_SUCCESS;
     ok = ok && found > 0;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const bool timed = ok && found > 1 && hipStreamIsCapturing(stream, &cap) == hipSuccess &&
+                       cap == hipStreamCaptureStatusNone;
     int pick = -1;
-    for (int i = 0; ok && i < found && pick < 0; ++i)
-      if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kWorkspaceBytes)
+    float best = 0.0f;
+    void* flush = nullptr;
+    if (timed && hipMalloc(&flush, kFlushBytes) != hipSuccess) flush = nullptr;
+    for (int i = 0; ok && i < found; ++i) {
+      if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kWorkspaceBytes)
+        continue;
+      if (!timed) {
         pick = i;
+        break;
+      }
+      const float t = time_algo(h, q, res[i].algo, res[i].workspaceSize, x, w, y, flush, stream);
+      if (t > 0.0f && (pick < 0 || t < best)) {
+        pick = i;
+        best = t;
+      }
+    }
+    if (flush) (void)hipFree(flush);
     ok = ok && pick >= 0;
     if (ok) {
       q.algo = res[pick].algo;
@@ -132,7 +187,8 @@ extern "C" int llmk_linear(llmk_blas* h, const uint16_t* x, const uint16_t* w, u
     auto key = std::make_tuple(T, in_features, out_features);
     auto it = h->plans.find(key);
     if (it == h->plans.end()) {
-      const int st = make_plan(h, T, in_features, out_features, &p);
+      const int st = make_plan(h, T, in_features, out_features, x, w, y,
+                               static_cast<hipStream_t>(stream), &p);
       if (st != LLMK_OK) return st;
       h->plans.emplace(key, p);
     } else {

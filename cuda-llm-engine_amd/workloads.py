@@ -96,6 +96,50 @@ def bytes_argmax(n: int, vocab: int) -> int:
     return n * vocab * 2 + n * 4  # logits read once, one int32 per row written
 
 
+def bytes_linear(T: int, in_f: int, out_f: int) -> int:
+    return out_f * in_f * 2 + T * in_f * 2 + T * out_f * 2  # weights and x read once, y written
+
+
+def bytes_decode_step(lens: np.ndarray, layers: int = LAYERS) -> int:
+    """Sum of the algorithmic bytes of every kernel of one engine forward pass over one decode
+    row per sequence (context lengths `lens`, the new token included): embedding, per layer the
+    QKV projection, RoPE + K/V scatter from the QKV rows, attention, o projection, add+RMSNorm,
+    gate/up projection, SwiGLU, down projection, add+RMSNorm; then the lm head and argmax.
+    Activations count once as written and once as read, as they cross HBM between kernels."""
+    n = int(np.asarray(lens).size)
+    qdim, kvdim = N_HEADS * HEAD_DIM, N_KV * HEAD_DIM
+    qkv = qdim + 2 * kvdim
+    per_layer = (bytes_linear(n, HIDDEN, qkv)
+                 + n * qkv * 2 + n * qdim * 2 + 2 * n * kvdim * 2 + 2 * n * 4 + HEAD_DIM // 2 * 4
+                 + bytes_attention(lens)
+                 + bytes_linear(n, qdim, HIDDEN)
+                 + bytes_add_rmsnorm(n, HIDDEN)
+                 + bytes_linear(n, HIDDEN, 2 * INTER)
+                 + bytes_swiglu(n * INTER)
+                 + bytes_linear(n, INTER, HIDDEN)
+                 + bytes_add_rmsnorm(n, HIDDEN))
+    return (bytes_embedding(n, HIDDEN) + bytes_rmsnorm(n, HIDDEN) + layers * per_layer
+            + bytes_linear(n, HIDDEN, VOCAB) + bytes_argmax(n, VOCAB))
+
+
+def decode_step_rows(lens: np.ndarray, max_pages: int = 128, seed: int = SEED_BASE + 8):
+    """One decode row per sequence: a token id, position len - 1, and the sequence's block table
+    over pages assigned from a shuffled permutation (unused entries 0). Returns (tokens,
+    positions, tables [n, max_pages], number of pages used)."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, np.int64)
+    npages = (lens + PAGE - 1) // PAGE
+    total = int(npages.sum())
+    perm = rng.permutation(total).astype(np.int32)
+    tables = np.zeros((lens.size, max_pages), np.int32)
+    at = 0
+    for b, k in enumerate(npages):
+        tables[b, :k] = perm[at:at + k]
+        at += k
+    tokens = rng.integers(0, VOCAB, lens.size).astype(np.int32)
+    return tokens, (lens - 1).astype(np.int32), tables, total
+
+
 def attention_lens(n: int = 256, max_len: int = 2048, seed: int = SEED_BASE + 6) -> np.ndarray:
     """Sequence lengths uniform in [1, max_len] (the decode configuration's context lengths)."""
     return np.random.default_rng(seed).integers(1, max_len + 1, n)
