@@ -32,6 +32,7 @@ LLMK_ERR_ALIGNMENT = 10003
 LLMK_ERR_UNSUPPORTED = 10004
 LLMK_ERR_BLAS = 10005
 LLMK_ERR_IO = 10006
+LLMK_ERR_CAPACITY = 10007
 
 
 class LlmkError(RuntimeError):
@@ -100,6 +101,35 @@ class LayerWeights(ctypes.Structure):
     _fields_ = [(n, _vp) for n in NAMES]
 
 
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+
+class Request(ctypes.Structure):
+    """Mirror of ``struct llmk_request`` (ref: engine/scheduler.h:6-14)."""
+    _fields_ = [("id", _i), ("prompt", _i32p), ("prompt_len", _i), ("max_new", _i),
+                ("arrival_step", _i), ("output", _i32p), ("n_output", _i),
+                ("t_arrive_ms", _d), ("t_first_ms", _d), ("t_done_ms", _d)]
+
+
+class SchedStats(ctypes.Structure):
+    """Mirror of ``struct llmk_sched_stats`` (ref: engine/scheduler.h:16-22)."""
+    _fields_ = [("decode_steps", _i), ("total_words", _i), ("prefills", _i), ("max_batch", _i),
+                ("iterations", _i), ("total_ms", _d), ("mean_batch", _d), ("prefill_ms", _d),
+                ("decode_ms", _d)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+PREFILL_FN = ctypes.CFUNCTYPE(_i, _vp, _i32p, _i, _i32p, _i, _i32p)
+DECODE_FN = ctypes.CFUNCTYPE(_i, _vp, _i, _i32p, _i32p, _i32p, _i, _i32p)
+
+
+class SchedModel(ctypes.Structure):
+    """Mirror of ``struct llmk_sched_model``: the scheduler's view of the model."""
+    _fields_ = [("user", _vp), ("prefill", PREFILL_FN), ("decode", DECODE_FN)]
+
+
 _SIGS = {
     "llmk_error_string": (ctypes.c_char_p, [_i]),
     "llmk_version": (_i, []),
@@ -131,6 +161,19 @@ _SIGS = {
     "llmk_engine_forward": (_i, [_vp, _i, _i, _i, _vp]),
     "llmk_engine_buffer": (_vp, [_vp, _i, _i]),
     "llmk_engine_reset_pools": (_i, [_vp, _vp]),
+    "llmk_engine_forward_graph": (_i, [_vp, _i, _i, _i, _vp]),
+    "llmk_engine_tune": (_i, [_vp, _i, _i, _vp]),
+    "llmk_blas_tune": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "llmk_pages_create": (_i, [_i, ctypes.POINTER(_vp)]),
+    "llmk_pages_destroy": (None, [_vp]),
+    "llmk_pages_total": (_i, [_vp]),
+    "llmk_pages_num_free": (_i, [_vp]),
+    "llmk_pages_alloc": (_i, [_vp]),
+    "llmk_pages_release": (_i, [_vp, _i]),
+    "llmk_pages_set_free_list": (_i, [_vp, _i32p, _i]),
+    "llmk_scheduler_run": (_i, [ctypes.POINTER(Request), _i, _i, _i, _i, _vp,
+                                ctypes.POINTER(SchedModel), ctypes.POINTER(SchedStats)]),
+    "llmk_engine_sched_model": (_i, [_vp, _vp, ctypes.POINTER(SchedModel)]),
 }
 
 _lib = ctypes.CDLL(LIB_PATH)
@@ -515,6 +558,17 @@ def linear(handle: Blas, x, w, y, T: int, in_features: int, out_features: int,
                                 _stream(stream)))
 
 
+def blas_tune(handle: Blas, x, w, y, T: int, in_features: int, out_features: int,
+              stream=None) -> None:
+    """Chooses the algorithm of one projection shape by timing (``llmk_blas_tune``)."""
+    fn = "blas_tune"
+    px = _dev(fn, x, torch.float16, T * in_features, "x")
+    pw = _dev(fn, w, torch.float16, out_features * in_features, "w")
+    py = _dev(fn, y, torch.float16, T * out_features, "y")
+    _check(fn, _lib.llmk_blas_tune(handle.handle, px, pw, py, T, in_features, out_features,
+                                   _stream(stream)))
+
+
 def qkv_rope_scatter(qkv, ld: int, q_out, k_pool, v_pool, block_tables, positions, inv_freq,
                      n: int, max_pages: int, page_size: int, n_heads: int, n_kv_heads: int,
                      head_dim: int, stream=None, check_indices: bool = True) -> None:
@@ -652,6 +706,26 @@ class Engine:
         _check("engine_forward", _lib.llmk_engine_forward(self._e, n_rows, n_logit_rows,
                                                           num_splits, _stream(stream)))
 
+    def forward_graph(self, n_rows: int, n_logit_rows: int = -1, num_splits: int = 0,
+                      stream=None) -> None:
+        """forward() through the engine's HIP graph cache (``llmk_engine_forward_graph``);
+        `stream` must not be the null stream."""
+        _check("engine_forward_graph", _lib.llmk_engine_forward_graph(
+            self._e, n_rows, n_logit_rows, num_splits, _stream(stream)))
+
+    def tune(self, n_rows: int, n_logit_rows: int = -1, stream=None) -> None:
+        """Times hipBLASLt's candidates for this row count's GEMM shapes (``llmk_engine_tune``)."""
+        _check("engine_tune", _lib.llmk_engine_tune(self._e, n_rows, n_logit_rows,
+                                                    _stream(stream)))
+
+    def sched_model(self, stream) -> "SchedModel":
+        """Scheduler callbacks that run this engine on `stream` (``llmk_engine_sched_model``)."""
+        m = SchedModel()
+        _check("engine_sched_model", _lib.llmk_engine_sched_model(self._e, _stream(stream),
+                                                                  ctypes.byref(m)))
+        m._engine = self  # keep the engine alive while the callbacks may run
+        return m
+
     def reset_pools(self, stream=None) -> None:
         _check("engine_reset_pools", _lib.llmk_engine_reset_pools(self._e, _stream(stream)))
 
@@ -693,3 +767,119 @@ class Engine:
             _fail("engine_write_pool", f"src must be a contiguous float16 tensor of {n} elements")
         torch.cuda.synchronize()
         _hip_memcpy(self.buffer_ptr(which, layer), src.data_ptr(), 2 * n)
+
+
+# ---------------------------------------------------------------------------------------------
+# continuous batching (ref: engine/paging.h, engine/scheduler.h)
+# ---------------------------------------------------------------------------------------------
+class PageAllocator:
+    """Page numbers from a free list (``llmk_page_allocator``; ref: engine/paging.h:7-23)."""
+
+    def __init__(self, num_pages: int):
+        a = _vp()
+        _check("pages_create", _lib.llmk_pages_create(num_pages, ctypes.byref(a)))
+        self._a = a
+
+    @property
+    def handle(self) -> int:
+        return self._a.value
+
+    @property
+    def total(self) -> int:
+        return _lib.llmk_pages_total(self._a)
+
+    def num_free(self) -> int:
+        return _lib.llmk_pages_num_free(self._a)
+
+    def alloc(self) -> int:
+        return _lib.llmk_pages_alloc(self._a)
+
+    def release(self, page: int) -> None:
+        _check("pages_release", _lib.llmk_pages_release(self._a, page))
+
+    def set_free_list(self, order) -> None:
+        import numpy as np
+        o = np.ascontiguousarray(order, np.int32)
+        _check("pages_set_free_list", _lib.llmk_pages_set_free_list(
+            self._a, o.ctypes.data_as(_i32p), o.size))
+
+    def close(self) -> None:
+        if self._a:
+            _lib.llmk_pages_destroy(self._a)
+            self._a = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def python_sched_model(prefill, decode) -> SchedModel:
+    """Wraps Python callables as scheduler callbacks: prefill(table: np.ndarray[max_pages],
+    prompt: np.ndarray) -> int and decode(tokens, positions, tables [n, max_pages]) -> sequence
+    of n ints. An exception ends the run with LLMK_ERR_INVALID_VALUE (and is re-raised by
+    run_scheduler)."""
+    import numpy as np
+    m = SchedModel()
+    m._errors = []
+
+    def _prefill(user, table, max_pages, prompt, n, out):
+        try:
+            t = np.ctypeslib.as_array(table, (max_pages,)).copy()
+            pr = np.ctypeslib.as_array(prompt, (n,)).copy()
+            out[0] = int(prefill(t, pr))
+            return 0
+        except BaseException as exc:  # noqa: BLE001 - reported after the run
+            m._errors.append(exc)
+            return LLMK_ERR_INVALID_VALUE
+
+    def _decode(user, n, tokens, positions, tables, max_pages, out):
+        try:
+            tok = np.ctypeslib.as_array(tokens, (n,)).copy()
+            pos = np.ctypeslib.as_array(positions, (n,)).copy()
+            tab = np.ctypeslib.as_array(tables, (n * max_pages,)).reshape(n, max_pages).copy()
+            res = list(decode(tok, pos, tab))
+            if len(res) != n:
+                raise ValueError(f"decode returned {len(res)} tokens for {n} rows")
+            for i, v in enumerate(res):
+                out[i] = int(v)
+            return 0
+        except BaseException as exc:  # noqa: BLE001 - reported after the run
+            m._errors.append(exc)
+            return LLMK_ERR_INVALID_VALUE
+
+    m._fns = (PREFILL_FN(_prefill), DECODE_FN(_decode))
+    m.prefill, m.decode = m._fns
+    return m
+
+
+def run_scheduler(requests, max_running: int, max_pages: int, page_size: int,
+                  pages: PageAllocator, model: SchedModel):
+    """Runs ``llmk_scheduler_run``. requests: list of dicts with prompt (ints), max_new,
+    arrival_step and optionally id, sorted by arrival_step. Returns (outputs: list of lists,
+    stats: dict, times: list of (t_arrive, t_first, t_done) ms)."""
+    import numpy as np
+    n = len(requests)
+    arr = (Request * max(1, n))()
+    keep = []
+    for i, r in enumerate(requests):
+        pr = np.ascontiguousarray(r["prompt"], np.int32)
+        out = np.zeros(max(1, int(r["max_new"])), np.int32)
+        keep += [pr, out]
+        arr[i].id = int(r.get("id", i))
+        arr[i].prompt = pr.ctypes.data_as(_i32p)
+        arr[i].prompt_len = pr.size
+        arr[i].max_new = int(r["max_new"])
+        arr[i].arrival_step = int(r.get("arrival_step", 0))
+        arr[i].output = out.ctypes.data_as(_i32p)
+    st = SchedStats()
+    status = _lib.llmk_scheduler_run(arr, n, max_running, max_pages, page_size, pages.handle,
+                                     ctypes.byref(model), ctypes.byref(st))
+    errors = getattr(model, "_errors", [])
+    if errors:
+        raise errors[0]
+    _check("scheduler_run", status)
+    outputs = [list(keep[2 * i + 1][:arr[i].n_output]) for i in range(n)]
+    times = [(arr[i].t_arrive_ms, arr[i].t_first_ms, arr[i].t_done_ms) for i in range(n)]
+    return outputs, st.as_dict(), times

@@ -35,7 +35,9 @@
 #include <string.h>
 #include <unistd.h>
 
+#include <map>
 #include <string>
+#include <tuple>
 #include <unordered_map>
 #include <vector>
 
@@ -85,6 +87,14 @@ struct llmk_engine {
            *proj = nullptr, *gu = nullptr, *act = nullptr, *fin = nullptr, *logits = nullptr;
   int32_t* next = nullptr;
   float* ws = nullptr;
+
+  // HIP graphs of the forward pass, keyed by (n_rows, n_logit_rows, num_splits)
+  struct Graph {
+    bool seen = false;
+    hipGraphExec_t exec = nullptr;
+  };
+  std::map<std::tuple<int, int, int>, Graph> graphs;
+  hipStream_t sched_stream = nullptr;  // the stream the scheduler callbacks run on
 };
 
 namespace {
@@ -160,6 +170,8 @@ void carve_activations(llmk_engine* e, Carver& c) {
 }
 
 void release(llmk_engine* e) {
+  for (auto& kv : e->graphs)
+    if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
   if (e->blas) llmk_blas_destroy(e->blas);
   if (e->wbuf) (void)hipFree(e->wbuf);
   if (e->pool_buf) (void)hipFree(e->pool_buf);
@@ -490,4 +502,125 @@ extern "C" int llmk_engine_reset_pools(llmk_engine* e, void* stream) {
   if (!e->pool_buf) return LLMK_OK;
   return (int)hipMemsetAsync(e->pool_buf, 0x7F, 2 * (size_t)e->cfg.n_layers * e->pool_elems * 2,
                              static_cast<hipStream_t>(stream));
+}
+
+extern "C" int llmk_engine_forward_graph(llmk_engine* e, int n_rows, int n_logit_rows,
+                                         int num_splits, void* stream) {
+  if (!e || !stream) return LLMK_ERR_INVALID_VALUE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  int st = (int)hipStreamIsCapturing(s, &cap);
+  if (st != LLMK_OK) return st;
+  if (cap != hipStreamCaptureStatusNone) return LLMK_ERR_INVALID_VALUE;
+  if (n_rows < 0 || n_rows > e->max_rows || n_logit_rows > n_rows) return LLMK_ERR_INVALID_VALUE;
+  if (n_rows == 0) return LLMK_OK;
+  llmk_engine::Graph& g = e->graphs[std::make_tuple(n_rows, n_logit_rows < 0 ? -1 : n_logit_rows,
+                                                    num_splits)];
+  if (g.exec) return (int)hipGraphLaunch(g.exec, s);
+  if (!g.seen) {  // first use: eager, which also makes the GEMM plans of these shapes
+    g.seen = true;
+    return llmk_engine_forward(e, n_rows, n_logit_rows, num_splits, stream);
+  }
+  st = (int)hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (st != LLMK_OK) return st;
+  const int fwd = llmk_engine_forward(e, n_rows, n_logit_rows, num_splits, stream);
+  hipGraph_t graph = nullptr;
+  st = (int)hipStreamEndCapture(s, &graph);
+  if (fwd != LLMK_OK || st != LLMK_OK) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return fwd != LLMK_OK ? fwd : st;
+  }
+  st = (int)hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (st != LLMK_OK) {
+    g.exec = nullptr;
+    return st;
+  }
+  return (int)hipGraphLaunch(g.exec, s);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Scheduler callbacks (llmk_sched_model) backed by the engine.
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+int read_tokens(llmk_engine* e, int32_t* dst, int n) {
+  int st = (int)hipMemcpyAsync(dst, e->next, (size_t)n * sizeof(int32_t), hipMemcpyDeviceToHost,
+                               e->sched_stream);
+  if (st == LLMK_OK) st = (int)hipStreamSynchronize(e->sched_stream);
+  return st;
+}
+
+// A prompt as rows at positions 0 .. len-1, in chunks of at most max_rows rows; only the last
+// chunk's last row goes through the lm head (ref: engine/paged.cu:111-127, model_prefill_paged).
+int sched_prefill(void* user, const int32_t* table, int max_pages, const int32_t* prompt, int len,
+                  int32_t* next_token) {
+  llmk_engine* e = static_cast<llmk_engine*>(user);
+  if (!table || !prompt || !next_token || len <= 0 || max_pages != e->max_pages)
+    return LLMK_ERR_INVALID_VALUE;
+  std::vector<int32_t> pos, tab;
+  for (int s0 = 0; s0 < len; s0 += e->max_rows) {
+    const int n = len - s0 < e->max_rows ? len - s0 : e->max_rows;
+    const bool last = s0 + n == len;
+    pos.resize(n);
+    tab.resize((size_t)n * max_pages);
+    for (int r = 0; r < n; ++r) {
+      pos[r] = s0 + r;
+      memcpy(&tab[(size_t)r * max_pages], table, (size_t)max_pages * sizeof(int32_t));
+    }
+    const int32_t lr = n - 1;
+    int st = llmk_engine_set_rows(e, n, prompt + s0, pos.data(), tab.data(), last ? 1 : 0,
+                                  last ? &lr : nullptr, e->sched_stream);
+    if (st == LLMK_OK) st = llmk_engine_forward(e, n, last ? 1 : 0, 0, e->sched_stream);
+    if (st != LLMK_OK) return st;
+  }
+  return read_tokens(e, next_token, 1);
+}
+
+int sched_decode(void* user, int n, const int32_t* tokens, const int32_t* positions,
+                 const int32_t* tables, int max_pages, int32_t* next_tokens) {
+  llmk_engine* e = static_cast<llmk_engine*>(user);
+  if (n <= 0 || n > e->max_rows || max_pages != e->max_pages || !next_tokens)
+    return LLMK_ERR_INVALID_VALUE;
+  int st = llmk_engine_set_rows(e, n, tokens, positions, tables, 0, nullptr, e->sched_stream);
+  if (st != LLMK_OK) return st;
+  st = e->sched_stream ? llmk_engine_forward_graph(e, n, -1, 0, e->sched_stream)
+                       : llmk_engine_forward(e, n, -1, 0, e->sched_stream);
+  if (st != LLMK_OK) return st;
+  return read_tokens(e, next_tokens, n);
+}
+
+}  // namespace
+
+extern "C" int llmk_engine_sched_model(llmk_engine* e, void* stream, llmk_sched_model* out) {
+  if (!e || !out) return LLMK_ERR_INVALID_VALUE;
+  e->sched_stream = static_cast<hipStream_t>(stream);
+  out->user = e;
+  out->prefill = sched_prefill;
+  out->decode = sched_decode;
+  return LLMK_OK;
+}
+
+extern "C" int llmk_engine_tune(llmk_engine* e, int n_rows, int n_logit_rows, void* stream) {
+  if (!e || n_rows <= 0 || n_rows > e->max_rows || n_logit_rows > n_rows)
+    return LLMK_ERR_INVALID_VALUE;
+  const llmk_model_config& m = e->cfg;
+  const int n = n_rows, H = m.hidden, nl = n_logit_rows < 0 ? n : n_logit_rows;
+  if (m.n_layers > 0) {
+    const LayerPtrs& w = e->layers[0];
+    const struct {
+      const uint16_t *x, *w;
+      uint16_t* y;
+      int in, out;
+    } shapes[] = {{e->normed, w.wqkv, e->qkv, H, e->qkvdim},
+                  {e->attn, w.wo, e->proj, e->qdim, H},
+                  {e->normed, w.wgu, e->gu, H, 2 * m.inter},
+                  {e->act, w.wdown, e->proj, m.inter, H}};
+    for (const auto& g : shapes) {
+      const int st = llmk_blas_tune(e->blas, g.x, g.w, g.y, n, g.in, g.out, stream);
+      if (st != LLMK_OK) return st;
+    }
+  }
+  if (nl > 0) return llmk_blas_tune(e->blas, e->normed, e->embed, e->logits, nl, H, m.vocab, stream);
+  return LLMK_OK;
 }

@@ -7,21 +7,24 @@
 // y = op_T(W) * x -- the same formulation as the reference's cuBLAS call.
 //
 // A handle owns one hipBLASLt handle, a 32 MiB workspace allocated once at creation, and a
-// cache of per-shape plans (descriptors, layouts and the chosen algorithm). The plan is made on
-// the first call of a shape: up to kCandidates algorithms from hipBLASLt's heuristic are each
-// timed on the caller's stream with the caller's operands (y is overwritten, then computed
-// again by the real call), and the fastest is kept. Each timed run follows a 512 MiB write that
-// evicts the 256 MB Infinity Cache, because in a decode step every weight matrix arrives cold
-// from HBM (2.5 GB of weights stream through per step); with warm caches the ranking favours
-// small tiles that lose on cold data. The flush buffer lives only while a plan is made. When
-// the stream is being captured into a HIP graph the first candidate is taken untimed; later
-// calls only enqueue the GEMM.
+// cache of per-shape plans (descriptors, layouts and the chosen algorithm). The first call of a
+// shape takes the heuristic's first algorithm; later calls, including calls made while a stream
+// is being captured into a HIP graph, only enqueue the GEMM.
+//
+// llmk_blas_tune replaces a shape's plan with the fastest of up to kCandidates heuristic
+// algorithms, each timed on the caller's stream with the caller's operands (y is overwritten).
+// Each timed run follows a 512 MiB write that evicts the 256 MB Infinity Cache, because in a
+// decode step every weight matrix arrives cold from HBM (2.5 GB of weights stream through per
+// step); with warm caches the ranking favours small tiles that lose on cold data. Tuning costs
+// tens of milliseconds per shape, so it is for the shapes a caller repeats (its decode batch
+// sizes), not for every prompt length.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <vector>
 
 #include "llmk.h"
 
@@ -55,6 +58,7 @@ struct llmk_blas {
   int device = 0;
   std::mutex mu;
   std::map<std::tuple<int, int, int>, Plan> plans;
+  std::vector<Plan> retired;  // plans replaced by llmk_blas_tune
 };
 
 namespace {
@@ -86,10 +90,11 @@ float time_algo(llmk_blas* h, const Plan& q, const hipblasLtMatmulAlgo_t& algo, 
   return ok ? best : -1.0f;
 }
 
-// Builds the plan of one (T, in, out) shape, timing the candidates on `stream` with the call's
-// operands unless the stream is capturing. Returns LLMK_OK or LLMK_ERR_BLAS.
+// Builds the plan of one (T, in, out) shape: the heuristic's first algorithm, or with `tune`
+// the fastest candidate timed on `stream` with the call's operands (not while the stream is
+// capturing). Returns LLMK_OK or LLMK_ERR_BLAS.
 int make_plan(llmk_blas* h, int T, int in, int out, const void* x, const void* w, void* y,
-              hipStream_t stream, Plan* p) {
+              hipStream_t stream, bool tune, Plan* p) {
   Plan q;
   const hipblasOperation_t opA = HIPBLAS_OP_T, opB = HIPBLAS_OP_N;
   bool ok = hipblasLtMatmulDescCreate(&q.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) ==
@@ -115,7 +120,8 @@ int make_plan(llmk_blas* h, int T, int in, int out, const void* x, const void* w
                                          res, &found) == HIPBLAS_STATUS_SUCCESS;
     ok = ok && found > 0;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    const bool timed = ok && found > 1 && hipStreamIsCapturing(stream, &cap) == hipSuccess &&
+    const bool timed = tune && ok && found > 1 &&
+                       hipStreamIsCapturing(stream, &cap) == hipSuccess &&
                        cap == hipStreamCaptureStatusNone;
     int pick = -1;
     float best = 0.0f;
@@ -171,6 +177,7 @@ extern "C" int llmk_blas_create(llmk_blas** out) {
 extern "C" void llmk_blas_destroy(llmk_blas* h) {
   if (!h) return;
   for (auto& kv : h->plans) destroy_plan(kv.second);
+  for (auto& p : h->retired) destroy_plan(p);
   if (h->workspace) (void)hipFree(h->workspace);
   if (h->lt) hipblasLtDestroy(h->lt);
   delete h;
@@ -188,7 +195,7 @@ extern "C" int llmk_linear(llmk_blas* h, const uint16_t* x, const uint16_t* w, u
     auto it = h->plans.find(key);
     if (it == h->plans.end()) {
       const int st = make_plan(h, T, in_features, out_features, x, w, y,
-                               static_cast<hipStream_t>(stream), &p);
+                               static_cast<hipStream_t>(stream), false, &p);
       if (st != LLMK_OK) return st;
       h->plans.emplace(key, p);
     } else {
@@ -200,4 +207,30 @@ extern "C" int llmk_linear(llmk_blas* h, const uint16_t* x, const uint16_t* w, u
       hipblasLtMatmul(h->lt, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.algo,
                       h->workspace, p.ws, static_cast<hipStream_t>(stream));
   return st == HIPBLAS_STATUS_SUCCESS ? LLMK_OK : LLMK_ERR_BLAS;
+}
+
+extern "C" int llmk_blas_tune(llmk_blas* h, const uint16_t* x, const uint16_t* w, uint16_t* y,
+                              int T, int in_features, int out_features, void* stream) {
+  if (!h || T <= 0 || in_features <= 0 || out_features <= 0 || !x || !w || !y)
+    return LLMK_ERR_INVALID_VALUE;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap) != hipSuccess ||
+      cap != hipStreamCaptureStatusNone)
+    return LLMK_ERR_INVALID_VALUE;
+  std::lock_guard<std::mutex> lock(h->mu);
+  Plan p;
+  const int st = make_plan(h, T, in_features, out_features, x, w, y,
+                           static_cast<hipStream_t>(stream), true, &p);
+  if (st != LLMK_OK) return st;
+  auto key = std::make_tuple(T, in_features, out_features);
+  auto it = h->plans.find(key);
+  if (it != h->plans.end()) {
+    // A graph captured earlier may hold the old plan's algorithm by value; its descriptors are
+    // kept alive until the handle is destroyed.
+    h->retired.push_back(it->second);
+    it->second = p;
+  } else {
+    h->plans.emplace(key, p);
+  }
+  return LLMK_OK;
 }

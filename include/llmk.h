@@ -43,6 +43,7 @@ extern "C" {
 #define LLMK_ERR_UNSUPPORTED 10004   /* a shape outside what the kernels implement */
 #define LLMK_ERR_BLAS 10005          /* hipBLASLt refused or failed a GEMM */
 #define LLMK_ERR_IO 10006            /* a weight file is missing, short, or lacks a tensor */
+#define LLMK_ERR_CAPACITY 10007      /* a request can never fit in the page pool or block table */
 
 /* Human-readable name of a status code (LLMK_ERR_* or hipError_t). Never NULL. */
 LLMK_API const char* llmk_error_string(int status);
@@ -222,10 +223,17 @@ LLMK_API void llmk_blas_destroy(llmk_blas* h);
 
 /* y[T, out_features] = x[T, in_features] * W^T, W stored [out_features, in_features] row-major
  * (a PyTorch Linear without bias); fp16 in and out, fp32 accumulation. The first call of a shape
- * chooses the algorithm (not during graph capture); later calls only enqueue.
- * ref: kernels/linear.cuh:5-7, kernels/linear.cu:5-25 (linear; cublasHandle_t -> llmk_blas*). */
+ * takes hipBLASLt's heuristic choice (make that call outside graph capture); later calls only
+ * enqueue. ref: kernels/linear.cuh:5-7, kernels/linear.cu:5-25 (linear; cublasHandle_t ->
+ * llmk_blas*). */
 LLMK_API int llmk_linear(llmk_blas* h, const uint16_t* x, const uint16_t* w, uint16_t* y, int T,
                          int in_features, int out_features, void* stream);
+
+/* Chooses the algorithm of one shape by timing hipBLASLt's heuristic candidates with cold
+ * caches, on `stream` with these operands (y is overwritten; synchronous; not while the stream
+ * is capturing). Later llmk_linear calls of the shape use it. New entry point. */
+LLMK_API int llmk_blas_tune(llmk_blas* h, const uint16_t* x, const uint16_t* w, uint16_t* y,
+                            int T, int in_features, int out_features, void* stream);
 
 /* RoPE + KV scatter reading the rows of one fused QKV projection: row b of qkv (stride ld
  * elements) holds q [n_heads, head_dim] at column 0, k [n_kv_heads, head_dim] after it and v
@@ -319,6 +327,90 @@ LLMK_API void* llmk_engine_buffer(llmk_engine* e, int which, int layer);
 
 /* Refills every pool slot with 0x7F7F (fp16 NaN), as at creation. Not capturable. */
 LLMK_API int llmk_engine_reset_pools(llmk_engine* e, void* stream);
+
+/* Tunes the GEMM plans of a forward pass over n_rows rows with n_logit_rows logit rows (< 0:
+ * all rows) -- llmk_blas_tune on every projection shape. Overwrites the activation buffers (not
+ * the pools); call it between passes, for the row counts that will repeat (decode batches).
+ * Synchronous; not capturable. */
+LLMK_API int llmk_engine_tune(llmk_engine* e, int n_rows, int n_logit_rows, void* stream);
+
+/* llmk_engine_forward through a HIP graph cache keyed by (n_rows, n_logit_rows, num_splits):
+ * the first call of a key runs eagerly (choosing the GEMM plans), the second captures the pass
+ * on `stream` and instantiates it, later calls launch the instance. Same results as
+ * llmk_engine_forward. `stream` must not be the null stream (it cannot be captured) and must
+ * not be capturing already; the rows are whatever llmk_engine_set_rows uploaded last. */
+LLMK_API int llmk_engine_forward_graph(llmk_engine* e, int n_rows, int n_logit_rows,
+                                       int num_splits, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Continuous batching: page allocator and request scheduler (host code).
+ * ------------------------------------------------------------------------------------------ */
+
+/* Hands out page numbers of the pools from a free list; page 0 first, then ascending, until
+ * pages are released or the list is reordered (ref: engine/paging.h:7-23 PageAllocator).
+ * alloc returns -1 when no page is free; release rejects a page that is out of range or
+ * already free (LLMK_ERR_INVALID_VALUE; the reference does not check). set_free_list reorders
+ * the currently free pages (a permutation of them), as the reference's tests shuffle the free
+ * list (ref: tests/test_scheduler.cu:21-22). */
+typedef struct llmk_page_allocator llmk_page_allocator;
+LLMK_API int llmk_pages_create(int num_pages, llmk_page_allocator** out);
+LLMK_API void llmk_pages_destroy(llmk_page_allocator* a);
+LLMK_API int llmk_pages_total(const llmk_page_allocator* a);
+LLMK_API int llmk_pages_num_free(const llmk_page_allocator* a);
+LLMK_API int llmk_pages_alloc(llmk_page_allocator* a);
+LLMK_API int llmk_pages_release(llmk_page_allocator* a, int page);
+LLMK_API int llmk_pages_set_free_list(llmk_page_allocator* a, const int32_t* order, int n);
+
+/* One request (ref: engine/scheduler.h:6-14 Request). The caller fills id, prompt,
+ * prompt_len >= 1, max_new >= 1, arrival_step and an output buffer of max_new entries; the
+ * scheduler fills n_output and the times (milliseconds from the start of the run, -1 if never
+ * reached). */
+typedef struct llmk_request {
+  int id;
+  const int32_t* prompt;
+  int prompt_len;
+  int max_new;
+  int arrival_step;
+  int32_t* output;
+  int n_output;
+  double t_arrive_ms, t_first_ms, t_done_ms;
+} llmk_request;
+
+/* Totals of one run (ref: engine/scheduler.h:16-22 SchedulerStats). */
+typedef struct llmk_sched_stats {
+  int decode_steps, total_words, prefills, max_batch, iterations;
+  double total_ms, mean_batch, prefill_ms, decode_ms;
+} llmk_sched_stats;
+
+/* The model as the scheduler sees it. prefill: run prompt[0 .. len) at positions 0 .. len-1 of
+ * the sequence whose block table is table[max_pages], write the greedy next token. decode: run
+ * n rows (tokens[i] at positions[i] of the sequence with table row i of tables[n, max_pages]),
+ * write the n greedy next tokens. Both return LLMK_OK or an error code, which ends the run. */
+typedef struct llmk_sched_model {
+  void* user;
+  int (*prefill)(void* user, const int32_t* table, int max_pages, const int32_t* prompt, int len,
+                 int32_t* next_token);
+  int (*decode)(void* user, int n, const int32_t* tokens, const int32_t* positions,
+                const int32_t* tables, int max_pages, int32_t* next_tokens);
+} llmk_sched_model;
+
+/* Runs every request to completion with continuous batching: arrivals by iteration, at most one
+ * admission per iteration when max_running allows and the free pages minus the pages running
+ * requests may still take cover the request's whole length, the admitted prompt prefilled at
+ * once, then one batched decode step for all running requests; a request leaves with max_new
+ * tokens and its pages go back to `pages` at once. Requests sorted by arrival_step.
+ * LLMK_ERR_CAPACITY if a request can never fit (nothing running and still too few pages, or
+ * more pages than max_pages); every page is returned before an error is reported.
+ * ref: engine/scheduler.cu:15-106 (run_scheduler). */
+LLMK_API int llmk_scheduler_run(llmk_request* reqs, int n_reqs, int max_running, int max_pages,
+                                int page_size, llmk_page_allocator* pages,
+                                const llmk_sched_model* model, llmk_sched_stats* stats);
+
+/* Scheduler callbacks that run the engine on `stream` (not the null stream): prefill in chunks
+ * of at most max_rows rows (eager), decode through llmk_engine_forward_graph; the greedy tokens
+ * come from the engine's GPU argmax (the reference's gpu_argmax mode,
+ * ref: engine/batched.cu:146-150). The engine's block tables must have the same max_pages. */
+LLMK_API int llmk_engine_sched_model(llmk_engine* e, void* stream, llmk_sched_model* out);
 
 #ifdef __cplusplus
 } /* extern "C" */

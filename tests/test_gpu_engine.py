@@ -68,6 +68,22 @@ def test_linear_matches_oracle(llmk, orc, blas, T, K, N):
     assert bad == 0 and exact > 0.9
 
 
+def test_linear_after_tuning_matches_oracle(llmk, orc, blas):
+    """llmk_blas_tune swaps a shape's algorithm for the fastest timed candidate; the result
+    keeps the same bar."""
+    T, K, N = 256, 2048, 3072
+    rng = np.random.default_rng(0x5EED0205)
+    x, w = normal_f16(rng, (T, K)), normal_f16(rng, (N, K), std=0.02)
+    dx, dw = dev(x), dev(w)
+    y = torch.empty(T * N, dtype=torch.float16, device=DEV)
+    llmk.blas_tune(blas, dx, dw, y, T, K, N)
+    y.fill_(float("nan"))
+    llmk.linear(blas, dx, dw, y, T, K, N)
+    torch.cuda.synchronize()
+    bad, exact = linear_rule(host(y), orc.linear(x, w, T, K, N, threads=16).ravel())
+    assert bad == 0 and exact > 0.9
+
+
 def test_linear_rejects_bad_arguments(llmk, blas):
     x = torch.zeros(4, 64, dtype=torch.float16, device=DEV)
     with pytest.raises(llmk.LlmkError):
