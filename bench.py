@@ -55,6 +55,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
                     help="summarise rocprofv3 csv output of this bench instead of running it")
+    ap.add_argument("--summarize-step", metavar="TRACE_DIR",
+                    help="per-kernel time of one engine decode step from a rocprofv3 kernel trace "
+                         "of `bench.py --kernels step`")
     return ap.parse_args()
 
 
@@ -178,6 +181,44 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
               f"traffic_bytes={traffic:.0f} algorithmic_bytes={alg} ratio={traffic / alg:.4f}")
 
 
+def summarize_step(trace_dir):
+    """Kernels of the engine's decode step (the dispatches between the first and the last
+    embedding gather of 256 rows, i.e. the graph replays), grouped by kernel name and grid size:
+    launches per step, mean duration, and time per step."""
+    import csv
+    import glob
+    rows = []
+    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+
+    def grid(r):
+        return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+
+    starts = [i for i, r in enumerate(rows) if "k_embedding" in r["Kernel_Name"]
+              and grid(r) == 256 * 64]
+    if len(starts) < 3:
+        print("no decode steps found")
+        return
+    # whole steps, skipping the eager first pass; only the step's own kernels (libllmk and
+    # hipBLASLt), not the bench's spin or fill kernels in between
+    steps = [r for r in rows[starts[1]:starts[-1]]
+             if "llmk" in r["Kernel_Name"] or r["Kernel_Name"].startswith("Cijk")]
+    n_steps = len(starts) - 2
+    agg = {}
+    for r in steps:
+        key = (r["Kernel_Name"], grid(r))
+        agg.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print(f"# engine decode step (Llama-3.2-1B shape, 256 rows), {n_steps} graph replays")
+    print("# launches/step  mean_us  us/step  grid  kernel")
+    total = 0.0
+    for (name, g), d in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        per = sum(d) / n_steps
+        total += per
+        print(f"{len(d) / n_steps:8.2f} {sum(d) / len(d):9.2f} {per:9.1f} {g:9d}  {name[:100]}")
+    print(f"# sum of kernel time per step: {total:.1f} us")
+
+
 class Timer:
     """Two timed passes of `steps` launches each.
 
@@ -276,6 +317,9 @@ def main() -> int:
     args = parse_args()
     if args.summarize_profiles:
         summarize_profiles(*args.summarize_profiles)
+        return 0
+    if args.summarize_step:
+        summarize_step(args.summarize_step)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the kernels are single-GPU; this build has no "

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "llmk.hpp"
+#include "llmk_engine.hpp"
 #include "../../oracle/oracle.h"
 
 #define HIP_CHECK(x)                                                                      \
@@ -354,6 +355,103 @@ int main() {
     report("argmax_rows constant row -> 0, tie -> 0, last", got[4] == 0 && got[6] == 0 &&
                                                                got[5] == V - 1);
     (void)hipFree(d); (void)hipFree(dout);
+  }
+
+  // ---- linear (ref: tests/test_linear.cu:20-50): y = x W^T against the oracle's fp32
+  // accumulation, the reference's rule |d| <= 3e-3 + 8e-3 |e|.
+  {
+    const int T = 7, in = 2048, out = 3072;
+    std::mt19937 rng(5);
+    auto x = normal_f16((size_t)T * in, rng, 0.f, 1.f);
+    auto w = normal_f16((size_t)out * in, rng, 0.f, 0.02f);
+    std::vector<uint16_t> expected((size_t)T * out);
+    or_linear(x.data(), w.data(), expected.data(), T, in, out);
+    llmk_blas* handle = nullptr;
+    if (llmk_blas_create(&handle) != LLMK_OK) {
+      report("linear handle", false);
+    } else {
+      uint16_t* dx = to_dev(x);
+      uint16_t* dw = to_dev(w);
+      uint16_t* dy = to_dev(std::vector<uint16_t>(), (size_t)T * out, 0x7F);
+      linear(handle, reinterpret_cast<__half*>(dx), reinterpret_cast<__half*>(dw),
+             reinterpret_cast<__half*>(dy), T, in, out);
+      HIP_CHECK(hipDeviceSynchronize());
+      auto got = to_host(dy, (size_t)T * out);
+      size_t bad = 0;
+      for (size_t i = 0; i < got.size(); ++i) {
+        const double g = or_h2f(got[i]), e = or_h2f(expected[i]);
+        bad += !(std::fabs(g - e) <= 3e-3 + 8e-3 * std::fabs(e));
+      }
+      std::snprintf(detail, sizeof(detail), "(%zu outside)", bad);
+      report("linear within the reference's rule", bad == 0, detail);
+      (void)hipFree(dx); (void)hipFree(dw); (void)hipFree(dy);
+      llmk_blas_destroy(handle);
+    }
+  }
+
+  // ---- run_scheduler over the engine (ref: tests/test_scheduler.cu:14-76): a small Llama-3
+  // shape with seeded weights; the same requests one at a time and up to 3 at once give the
+  // same outputs, batching takes fewer decode steps, and every page comes back.
+  {
+    llmk_model_config cfg = llmk::llama32_1b_config();
+    cfg.n_layers = 2;
+    cfg.hidden = 256;
+    cfg.n_heads = 4;
+    cfg.n_kv_heads = 1;
+    cfg.inter = 512;
+    cfg.vocab = 512;
+    const int num_pages = 40, max_pages = 8;
+    llmk::Engine eng(cfg, 16, max_pages, num_pages);
+    std::mt19937 rng(9);
+    const int H = cfg.hidden, I = cfg.inter, qd = cfg.n_heads * 64, kvd = cfg.n_kv_heads * 64;
+    std::vector<std::vector<uint16_t>> keep;
+    auto add = [&](size_t n, float mean, float sd) {
+      keep.push_back(normal_f16(n, rng, mean, sd));
+      return reinterpret_cast<const uint16_t*>(keep.back().data());
+    };
+    const uint16_t* embed = add((size_t)cfg.vocab * H, 0.f, 0.5f);
+    const uint16_t* fnorm = add(H, 1.f, 0.1f);
+    std::vector<llmk_layer_weights> layers(cfg.n_layers);
+    for (auto& l : layers) {
+      l.attn_norm = add(H, 1.f, 0.1f);
+      l.wq = add((size_t)qd * H, 0.f, 0.05f);
+      l.wk = add((size_t)kvd * H, 0.f, 0.05f);
+      l.wv = add((size_t)kvd * H, 0.f, 0.05f);
+      l.wo = add((size_t)H * qd, 0.f, 0.05f);
+      l.mlp_norm = add(H, 1.f, 0.1f);
+      l.w_gate = add((size_t)I * H, 0.f, 0.05f);
+      l.w_up = add((size_t)I * H, 0.f, 0.05f);
+      l.w_down = add((size_t)H * I, 0.f, 0.05f);
+    }
+    eng.set_weights(reinterpret_cast<const __half*>(embed), reinterpret_cast<const __half*>(fnorm),
+                    layers);
+    std::vector<llmk::Request> base(9);
+    std::uniform_int_distribution<int> tok(0, cfg.vocab - 1), len(2, 40), nnew(1, 7);
+    for (int i = 0; i < 9; ++i) {
+      base[i].id = i;
+      base[i].prompt.resize(len(rng));
+      for (auto& t : base[i].prompt) t = tok(rng);
+      base[i].max_new = nnew(rng);
+      base[i].arrival_step = i;
+    }
+    hipStream_t stream;
+    HIP_CHECK(hipStreamCreate(&stream));
+    std::vector<llmk::Request> one = base, three = base;
+    llmk::PageAllocator pages(num_pages);
+    const llmk::SchedulerStats s1 = llmk::run_scheduler(eng, pages, one, 1, stream);
+    const int free1 = pages.num_free();
+    const llmk::SchedulerStats s3 = llmk::run_scheduler(eng, pages, three, 3, stream);
+    bool same = true;
+    for (int i = 0; i < 9; ++i)
+      same = same && one[i].output == three[i].output &&
+             (int)one[i].output.size() == base[i].max_new;
+    std::snprintf(detail, sizeof(detail), "(%d vs %d decode steps)", s1.decode_steps,
+                  s3.decode_steps);
+    report("run_scheduler: batched outputs = one at a time", same, detail);
+    report("run_scheduler: batching takes fewer steps", s3.decode_steps < s1.decode_steps);
+    report("run_scheduler: every page returned", free1 == num_pages &&
+                                                     pages.num_free() == num_pages);
+    HIP_CHECK(hipStreamDestroy(stream));
   }
 
   std::printf("%s: %d failure(s)\n", failures ? "FAILED" : "ALL PASSED", failures);
