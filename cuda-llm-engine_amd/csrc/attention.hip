@@ -86,47 +86,59 @@ constexpr int chunk_rows() {
   return kChunk * (8 / KVW) <= kPage ? kChunk : kPage / (8 / KVW);
 }
 
-// One chunk of row reads: rows [row0, row0 + ROWS) of this block's position range, all in one
-// page. FULL: every position in the chunk is cached (no per-lane tests).
-template <int KVW, bool FULL>
-__device__ __forceinline__ void attend_chunk(SoftmaxState& st, const u32x4 (&qv)[kGroup],
-                                             const f16* __restrict__ k_pool,
-                                             const f16* __restrict__ v_pool,
-                                             const int* __restrict__ table, int pos0, int pos1,
-                                             int row0, size_t row_halves, size_t lane_off,
-                                             int slot) {
-  constexpr int PPL = 8 / KVW;  // positions per row read
-  constexpr int ROWS = chunk_rows<KVW>();
-  const int cpos = pos0 + row0 * PPL;  // first position of the chunk (wave-uniform)
+// The row reads of one chunk, K and V.
+template <int KVW>
+struct Chunk {
+  static constexpr int ROWS = chunk_rows<KVW>();
+  u32x4 k[ROWS], v[ROWS];
+};
+
+// Element offset of the first row of the chunk that starts at row `row0` of the block's position
+// range [pos0, ...): its page from the block table (wave-uniform, so the pool address of the
+// chunk stays in scalar registers and each lane adds only its 32-bit offset).
+template <int KVW>
+__device__ __forceinline__ size_t chunk_base(const int* __restrict__ table, int pos0, int row0,
+                                             size_t row_halves) {
+  const int cpos = pos0 + row0 * (8 / KVW);  // first position of the chunk
   const int page = table[cpos / kPage];
-  const size_t base = ((size_t)page * kPage + (size_t)(cpos % kPage)) * row_halves + lane_off;
-  u32x4 kr[ROWS], vr[ROWS];
-  bool ok[ROWS];
+  return ((size_t)page * kPage + (size_t)(cpos % kPage)) * row_halves;
+}
+
+// Issues the loads of a chunk whose every position is cached (unconditional, so that the loads
+// of the next chunk can be in flight while this one is folded). lane_off: the lane's element
+// offset inside the first row; row_step: elements from one row read to the next.
+template <int KVW>
+__device__ __forceinline__ void load_chunk(Chunk<KVW>& c, const f16* __restrict__ k_pool,
+                                           const f16* __restrict__ v_pool,
+                                           const int* __restrict__ table, int pos0, int row0,
+                                           size_t row_halves, uint32_t lane_off,
+                                           uint32_t row_step) {
+  const size_t base = chunk_base<KVW>(table, pos0, row0, row_halves);
+  const f16* kb = k_pool + base;
+  const f16* vb = v_pool + base;
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r) {
-    const size_t off = base + (size_t)(r * PPL) * row_halves;
-    ok[r] = FULL || cpos + r * PPL + slot < pos1;
-    if (FULL) {
-      kr[r] = ld16_stream(k_pool + off);
-      vr[r] = ld16_stream(v_pool + off);
-    } else {
-      const u32x4 zero = {0u, 0u, 0u, 0u};
-      kr[r] = zero;
-      vr[r] = zero;
-      if (ok[r]) {
-        kr[r] = ld16_stream(k_pool + off);
-        vr[r] = ld16_stream(v_pool + off);
-      }
-    }
+  for (int r = 0; r < Chunk<KVW>::ROWS; ++r) {
+    const uint32_t off = lane_off + (uint32_t)r * row_step;
+    c.k[r] = ld16_stream(kb + off);
+    c.v[r] = ld16_stream(vb + off);
   }
+}
+
+// Folds a loaded chunk into the online softmax. FULL: every position of the chunk is cached;
+// otherwise ok[r] says whether the lane's position of row read r is.
+template <int KVW, bool FULL>
+__device__ __forceinline__ void fold_chunk(SoftmaxState& st, const u32x4 (&qv)[kGroup],
+                                           const Chunk<KVW>& c,
+                                           const bool (&ok)[Chunk<KVW>::ROWS]) {
+  constexpr int ROWS = Chunk<KVW>::ROWS;
   // Raw scores q.k (uncached positions: -inf); the scale is applied inside the exponent.
   float s[ROWS][kGroup];
 #pragma unroll
   for (int r = 0; r < ROWS; ++r)
 #pragma unroll
     for (int i = 0; i < kGroup; ++i) {
-      const float d = octet_sum(dot8(qv[i], kr[r]));
-      s[r][i] = ok[r] ? d : -INFINITY;
+      const float d = octet_sum(dot8(qv[i], c.k[r]));
+      s[r][i] = FULL || ok[r] ? d : -INFINITY;
     }
   float corr[kGroup], p[ROWS][kGroup];
   bool grew = false;
@@ -158,7 +170,7 @@ __device__ __forceinline__ void attend_chunk(SoftmaxState& st, const u32x4 (&qv)
   }
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
-    const f16x8 vh = as_h8(vr[r]);
+    const f16x8 vh = as_h8(c.v[r]);
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const float v = (float)vh[d];
@@ -166,6 +178,38 @@ __device__ __forceinline__ void attend_chunk(SoftmaxState& st, const u32x4 (&qv)
       for (int i = 0; i < kGroup; ++i) st.acc[i][d] = __builtin_fmaf(p[r][i], v, st.acc[i][d]);
     }
   }
+}
+
+// The one chunk of a wave that holds uncached positions: rows [row0, row0 + ROWS) of the block's
+// range [pos0, pos1), only the cached positions loaded.
+template <int KVW>
+__device__ __forceinline__ void attend_partial_chunk(SoftmaxState& st,
+                                                     const u32x4 (&qv)[kGroup],
+                                                     const f16* __restrict__ k_pool,
+                                                     const f16* __restrict__ v_pool,
+                                                     const int* __restrict__ table, int pos0,
+                                                     int pos1, int row0, size_t row_halves,
+                                                     uint32_t lane_off, uint32_t row_step,
+                                                     int slot) {
+  constexpr int PPL = 8 / KVW;
+  constexpr int ROWS = Chunk<KVW>::ROWS;
+  const int cpos = pos0 + row0 * PPL;
+  const size_t base = chunk_base<KVW>(table, pos0, row0, row_halves);
+  Chunk<KVW> c;
+  bool ok[ROWS];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const uint32_t off = lane_off + (uint32_t)r * row_step;
+    ok[r] = cpos + r * PPL + slot < pos1;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    c.k[r] = zero;
+    c.v[r] = zero;
+    if (ok[r]) {
+      c.k[r] = ld16_stream(k_pool + base + off);
+      c.v[r] = ld16_stream(v_pool + base + off);
+    }
+  }
+  fold_chunk<KVW, false>(st, qv, c, ok);
 }
 
 // Per-block LDS: the waves' softmax states for the merge at the end of a segment.
@@ -201,7 +245,8 @@ __device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
   const size_t row_halves = (size_t)n_kv_heads * kHeadDim;
   // Lane's offset inside a row read: this kv group's 8 heads, then 16 bytes per lane (for
   // KVW < 8 the lanes run on into the next PPL - 1 rows, which are contiguous within a page).
-  const size_t lane_off = (size_t)kvg * 8 * kHeadDim + (size_t)lane * 8;
+  const uint32_t lane_off = (uint32_t)(kvg * 8 * kHeadDim + lane * 8);
+  const uint32_t row_step = (uint32_t)(PPL * row_halves);
 
   u32x4 qv[kGroup];
 #pragma unroll
@@ -219,13 +264,42 @@ __device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
 
   const int n_rows = (pos1 - pos0 + PPL - 1) / PPL;
   const int full_rows = (pos1 - pos0) / PPL;  // rows whose every position is cached
-  int row0 = wave * ROWS;
-  for (; row0 + ROWS <= full_rows; row0 += kWaves * ROWS)
-    attend_chunk<KVW, true>(st, qv, k_pool, v_pool, table, pos0, pos1, row0, row_halves,
-                            lane_off, slot);
+  // The wave's chunks whose every position is cached start at rows first + j * STEP, j < nj.
+  // They are double-buffered: the loads of chunk j + 1 are issued before chunk j is folded. The
+  // steady loop issues its loads unconditionally; a conditional load would make the compiler
+  // wait for every outstanding load, the new ones included, before each fold.
+  constexpr int STEP = kWaves * ROWS;
+  const int first = wave * ROWS;
+  const int nj = first + ROWS <= full_rows ? (full_rows - first - ROWS) / STEP + 1 : 0;
+  bool all[ROWS];  // unused by the FULL fold
+#pragma unroll
+  for (int i = 0; i < ROWS; ++i) all[i] = true;
+  if (nj > 0) {
+    Chunk<KVW> a, b;
+    load_chunk<KVW>(a, k_pool, v_pool, table, pos0, first, row_halves, lane_off,
+                    row_step);
+    int j = 1, r = first + STEP;
+    for (; j + 1 < nj; j += 2, r += 2 * STEP) {
+      load_chunk<KVW>(b, k_pool, v_pool, table, pos0, r, row_halves, lane_off,
+                      row_step);
+      fold_chunk<KVW, true>(st, qv, a, all);
+      load_chunk<KVW>(a, k_pool, v_pool, table, pos0, r + STEP, row_halves,
+                      lane_off, row_step);
+      fold_chunk<KVW, true>(st, qv, b, all);
+    }
+    if (j < nj) {
+      load_chunk<KVW>(b, k_pool, v_pool, table, pos0, r, row_halves, lane_off,
+                      row_step);
+      fold_chunk<KVW, true>(st, qv, a, all);
+      fold_chunk<KVW, true>(st, qv, b, all);
+    } else {
+      fold_chunk<KVW, true>(st, qv, a, all);
+    }
+  }
+  const int row0 = first + nj * STEP;
   if (row0 < n_rows)  // at most one partly cached chunk per wave
-    attend_chunk<KVW, false>(st, qv, k_pool, v_pool, table, pos0, pos1, row0, row_halves,
-                             lane_off, slot);
+    attend_partial_chunk<KVW>(st, qv, k_pool, v_pool, table, pos0, pos1, row0, row_halves,
+                              lane_off, row_step, slot);
 
   // Merge the NP partial states of every query head through LDS.
   const int pi = wave * PPL + slot;
