@@ -90,9 +90,10 @@ PROFILE_SHAPES = [
     ("swiglu_8192x8192", "k_swiglu_vecILi2E", 16384 * 256, 402653184),
     ("embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
     ("copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),
-    ("attention_decode_256", "k_attn_balancedILi8E", 1024 * 256, ATTN_BYTES_256,
+    # 512 blocks: two resident blocks of 256 threads on each of the 256 CUs (191 VGPRs).
+    ("attention_decode_256", "k_attn_balancedILi8E", 512 * 256, ATTN_BYTES_256,
      ("k_attn_merge", 256 * 256)),
-    ("attention_decode_16x2048", "k_attn_balancedILi8E", 1024 * 256, ATTN_BYTES_16x2048,
+    ("attention_decode_16x2048", "k_attn_balancedILi8E", 512 * 256, ATTN_BYTES_16x2048,
      ("k_attn_merge", 256 * 16)),
     ("argmax_256x128256", "k_argmax_vec", 256 * 1024, 256 * 128256 * 2 + 256 * 4),
     ("decode:embedding_256", "k_embeddingILi0E", 256 * 64, 2098176),

@@ -12,7 +12,10 @@
 // is being captured into a HIP graph, only enqueue the GEMM.
 //
 // llmk_blas_tune replaces a shape's plan with the fastest of up to kCandidates heuristic
-// algorithms, each timed on the caller's stream with the caller's operands (y is overwritten).
+// algorithms, each timed on the caller's stream with the caller's operands (y is overwritten):
+// every candidate by its best of kTimedRuns launches, then the kFinalists fastest again by the
+// median of kFinalRuns launches (a single cold launch of a 10-30 us GEMM varies by several
+// percent, enough to swap plans that differ by 10% inside a decode step).
 // Each timed run follows a 512 MiB write that evicts the 256 MB Infinity Cache, because in a
 // decode step every weight matrix arrives cold from HBM (2.5 GB of weights stream through per
 // step); with warm caches the ranking favours small tiles that lose on cold data. Tuning costs
@@ -21,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -33,6 +37,8 @@ namespace {
 constexpr size_t kWorkspaceBytes = 32u << 20;
 constexpr int kCandidates = 128;  // heuristic results considered per shape
 constexpr int kTimedRuns = 3;     // timed cold launches per candidate (after one untimed)
+constexpr int kFinalists = 4;     // candidates timed again
+constexpr int kFinalRuns = 15;    // timed cold launches per finalist (median taken)
 constexpr size_t kFlushBytes = 512u << 20;
 
 struct Plan {
@@ -63,10 +69,12 @@ struct llmk_blas {
 
 namespace {
 
-// Smallest duration of kTimedRuns cold launches of one algorithm (each after a write of the
-// flush buffer, when there is one), or a negative value if it fails to run.
+// Smallest (median: false) or median (true) duration of `runs` cold launches of one algorithm
+// (each after a write of the flush buffer, when there is one), or a negative value if it fails
+// to run.
 float time_algo(llmk_blas* h, const Plan& q, const hipblasLtMatmulAlgo_t& algo, size_t ws,
-                const void* x, const void* w, void* y, void* flush, hipStream_t stream) {
+                const void* x, const void* w, void* y, void* flush, hipStream_t stream, int runs,
+                bool median) {
   const float alpha = 1.0f, beta = 0.0f;
   auto run = [&] {
     return hipblasLtMatmul(h->lt, q.desc, &alpha, w, q.a, x, q.b, &beta, y, q.d, y, q.d, &algo,
@@ -75,19 +83,21 @@ float time_algo(llmk_blas* h, const Plan& q, const hipblasLtMatmulAlgo_t& algo, 
   if (!run()) return -1.0f;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0f;
-  float best = -1.0f;
+  std::vector<float> t;
   bool ok = true;
-  for (int i = 0; ok && i < kTimedRuns; ++i) {
+  for (int i = 0; ok && i < runs; ++i) {
     if (flush) ok = hipMemsetAsync(flush, i & 0xFF, kFlushBytes, stream) == hipSuccess;
     ok = ok && hipEventRecord(e0, stream) == hipSuccess && run() &&
          hipEventRecord(e1, stream) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
     float ms = 0.0f;
     ok = ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
-    if (ok && (best < 0.0f || ms < best)) best = ms;
+    if (ok) t.push_back(ms);
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
-  return ok ? best : -1.0f;
+  if (!ok || t.empty()) return -1.0f;
+  std::sort(t.begin(), t.end());
+  return median ? t[t.size() / 2] : t[0];
 }
 
 // Builds the plan of one (T, in, out) shape: the heuristic's first algorithm, or with `tune`
@@ -124,9 +134,9 @@ int make_plan(llmk_blas* h, int T, int in, int out, const void* x, const void* w
                        hipStreamIsCapturing(stream, &cap) == hipSuccess &&
                        cap == hipStreamCaptureStatusNone;
     int pick = -1;
-    float best = 0.0f;
     void* flush = nullptr;
     if (timed && hipMalloc(&flush, kFlushBytes) != hipSuccess) flush = nullptr;
+    std::vector<std::pair<float, int>> first;  // (best of kTimedRuns, candidate)
     for (int i = 0; ok && i < found; ++i) {
       if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kWorkspaceBytes)
         continue;
@@ -134,10 +144,21 @@ int make_plan(llmk_blas* h, int T, int in, int out, const void* x, const void* w
         pick = i;
         break;
       }
-      const float t = time_algo(h, q, res[i].algo, res[i].workspaceSize, x, w, y, flush, stream);
-      if (t > 0.0f && (pick < 0 || t < best)) {
-        pick = i;
-        best = t;
+      const float t = time_algo(h, q, res[i].algo, res[i].workspaceSize, x, w, y, flush, stream,
+                                kTimedRuns, false);
+      if (t > 0.0f) first.emplace_back(t, i);
+    }
+    if (timed && !first.empty()) {
+      std::sort(first.begin(), first.end());
+      float best = 0.0f;
+      for (size_t f = 0; f < first.size() && f < (size_t)kFinalists; ++f) {
+        const int i = first[f].second;
+        const float t = time_algo(h, q, res[i].algo, res[i].workspaceSize, x, w, y, flush,
+                                  stream, kFinalRuns, true);
+        if (t > 0.0f && (pick < 0 || t < best)) {
+          pick = i;
+          best = t;
+        }
       }
     }
     if (flush) (void)hipFree(flush);
