@@ -48,7 +48,7 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--kernels", choices=["all", "headline", "step"], default="all",
+    ap.add_argument("--kernels", choices=["all", "headline", "step", "sched"], default="all",
                     help="all: every configuration; headline: config 2 only; step: config 2 and "
                          "the engine's decode step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -367,6 +367,8 @@ def main() -> int:
 
     if args.kernels == "step":
         kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W))
+    if args.kernels == "sched":
+        kernels.update(bench_scheduler(llmk, wl, torch, np, dev))
 
     if args.kernels == "all":
         # config 1: RMSNorm [16, 2048] (the reference's CPU-plumbing case, on the GPU)
@@ -496,6 +498,10 @@ def main() -> int:
         # graph per step (ref: engine/batched.cu:81-120, model_decode_batch_greedy :146-150)
         kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W))
 
+        # continuous batching on the engine: the reference's scheduler workload, one request
+        # at a time and up to 8 at once (ref: tests/test_scheduler.cu, engine/scheduler.cu)
+        kernels.update(bench_scheduler(llmk, wl, torch, np, dev))
+
         # copy probe: practical HBM ceiling (ref: bench/bandwidth.cu)
         nb = 1 << 30
         bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(4)]
@@ -576,6 +582,71 @@ def bench_decode_step(llmk, wl, timer, torch, np, dev, K, W) -> dict:
     del graph
     torch.cuda.empty_cache()
     return {"decode_step_1b_256": e}
+
+
+def bench_scheduler(llmk, wl, torch, np, dev) -> dict:
+    """The reference's scheduler benchmark on the engine (Llama-3.2-1B shape, seeded random
+    weights): 24 requests (prompts of 5 to 402 tokens, 32 new tokens each, one eligible every 2
+    iterations), 256 pages of 16, one request at a time and up to 8 at once, two rounds each as
+    the reference runs them (ref: tests/test_scheduler.cu:14-76). words/s = new tokens over the
+    scheduler's own wall clock (first iteration to last retirement), as the reference reports
+    it. Decode steps of each batch size run from the engine's HIP graph cache."""
+    import importlib
+    weights = importlib.import_module("llmk.weights")
+    cfg = llmk.ModelConfig()
+    max_len = max(wl.SCHED_PROMPT_LENS) + wl.SCHED_NEW
+    max_pages = (max_len + wl.PAGE - 1) // wl.PAGE
+    max_rows = 512  # the longest prompt (402 tokens) prefills in one pass
+    eng = llmk.Engine(cfg, max_rows=max_rows, max_pages=max_pages, num_pages=wl.SCHED_PAGES)
+    w = weights.random_weights(cfg, wl.SEED_BASE + 9, device=dev)
+    eng.set_weights(*weights.engine_layers(w, cfg))
+    del w
+    torch.cuda.empty_cache()
+    stream = torch.cuda.Stream()
+    model = eng.sched_model(stream)
+    reqs = wl.scheduler_requests()
+    order = np.random.default_rng(wl.SEED_BASE + 12).permutation(wl.SCHED_PAGES).astype(np.int32)
+
+    def run(rs, max_running):
+        pages = llmk.PageAllocator(wl.SCHED_PAGES)
+        pages.set_free_list(order)
+        outs, stats, _ = llmk.run_scheduler(rs, max_running, max_pages, wl.PAGE, pages, model)
+        if pages.num_free() != wl.SCHED_PAGES:
+            raise RuntimeError("scheduler run leaked pages")
+        return outs, stats
+
+    run(reqs[:2], wl.SCHED_MAX_RUNNING)  # warm-up, as the reference does
+    run(reqs[:wl.SCHED_MAX_RUNNING], wl.SCHED_MAX_RUNNING)  # captures the decode graphs
+    rounds = []
+    outputs = {}
+    for rnd in (1, 2):
+        for mr in (1, wl.SCHED_MAX_RUNNING):
+            outs, st = run(reqs, mr)
+            if mr in outputs and outputs[mr] != outs:
+                raise RuntimeError("scheduler outputs changed between rounds")
+            outputs[mr] = outs
+            wps = st["total_words"] / (st["total_ms"] * 1e-3)
+            rounds.append({"round": rnd, "max_running": mr, "decode_steps": st["decode_steps"],
+                           "mean_batch": round(st["mean_batch"], 2),
+                           "total_ms": round(st["total_ms"], 2),
+                           "prefill_ms": round(st["prefill_ms"], 2),
+                           "decode_ms": round(st["decode_ms"], 2),
+                           "words_per_s": round(wps, 1)})
+            log(f"  scheduler round {rnd}, up to {mr} at once: {st['decode_steps']} decode "
+                f"steps, mean batch {st['mean_batch']:.1f}, {st['total_ms']:.1f} ms, "
+                f"{wps:.0f} words/s")
+    if outputs[1] != outputs[wl.SCHED_MAX_RUNNING]:
+        raise RuntimeError("batched and one-at-a-time scheduler outputs differ")
+    best = {mr: max(r["words_per_s"] for r in rounds if r["max_running"] == mr)
+            for mr in (1, wl.SCHED_MAX_RUNNING)}
+    eng.close()
+    torch.cuda.empty_cache()
+    return {"scheduler_24x32_1b": {
+        "label": "continuous batching, 24 requests x 32 new tokens (Llama-3.2-1B shape)",
+        "words_per_s": best[wl.SCHED_MAX_RUNNING], "words_per_s_one_at_a_time": best[1],
+        "gain": round(best[wl.SCHED_MAX_RUNNING] / best[1], 2), "rounds": rounds,
+        "note": "reference on an RTX 4050 Laptop: 249 words/s up to 8 at once, 60 one at a "
+                "time (docs/scheduler_results.md); outputs identical in both modes"}}
 
 
 def cpu_baseline(inp, rows, hidden, nbytes, seconds, eps):

@@ -151,6 +151,7 @@ _SIGS = {
     "llmk_blas_create": (_i, [ctypes.POINTER(_vp)]),
     "llmk_blas_destroy": (None, [_vp]),
     "llmk_linear": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "llmk_linear_rows": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "llmk_qkv_rope_scatter": (_i, [_vp, _i] + [_vp] * 6 + [_i] * 6 + [_vp]),
     "llmk_swiglu_rows": (_i, [_vp, _vp, _i, _i, _vp]),
     "llmk_engine_create": (_i, [ctypes.POINTER(ModelConfig), _i, _i, _i, ctypes.POINTER(_vp)]),
@@ -556,6 +557,21 @@ def linear(handle: Blas, x, w, y, T: int, in_features: int, out_features: int,
     py = _dev(fn, y, torch.float16, T * out_features, "y")
     _check(fn, _lib.llmk_linear(handle.handle, px, pw, py, T, in_features, out_features,
                                 _stream(stream)))
+
+
+LINEAR_ROWS_MAX = 8  # LLMK_LINEAR_ROWS_MAX
+
+
+def linear_rows(x, w, y, T: int, in_features: int, out_features: int, stream=None) -> None:
+    """linear() for T <= 8 rows with this library's weight-streaming kernel
+    (``llmk_linear_rows``); in_features % 512 == 0."""
+    fn = "linear_rows"
+    if T < 0 or in_features <= 0 or out_features <= 0:
+        _fail(fn, "T must be >= 0 and the feature counts > 0")
+    px = _dev(fn, x, torch.float16, T * in_features, "x")
+    pw = _dev(fn, w, torch.float16, out_features * in_features, "w")
+    py = _dev(fn, y, torch.float16, T * out_features, "y")
+    _check(fn, _lib.llmk_linear_rows(px, pw, py, T, in_features, out_features, _stream(stream)))
 
 
 def blas_tune(handle: Blas, x, w, y, T: int, in_features: int, out_features: int,

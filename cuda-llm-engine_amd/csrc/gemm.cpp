@@ -2,9 +2,11 @@
 // PyTorch Linear without bias), fp16 in and out, fp32 accumulation. ref: kernels/linear.cuh:5-7,
 // kernels/linear.cu:5-25 (cublasGemmEx, CUBLAS_COMPUTE_32F).
 //
-// These are plain library GEMMs, so they go to hipBLASLt. Viewed column-major, the row-major
-// buffers are W: [in x out] (ld in), x: [in x T] (ld in), y: [out x T] (ld out), and
-// y = op_T(W) * x -- the same formulation as the reference's cuBLAS call.
+// These are plain library GEMMs, so they go to hipBLASLt, except with at most 8 rows (a decode
+// step with few sequences), where llmk_linear_rows (gemv.hip) streams the weights itself.
+// Viewed column-major, the row-major buffers are W: [in x out] (ld in), x: [in x T] (ld in),
+// y: [out x T] (ld out), and y = op_T(W) * x -- the same formulation as the reference's cuBLAS
+// call.
 //
 // A handle owns one hipBLASLt handle, a 32 MiB workspace allocated once at creation, and a
 // cache of per-shape plans (descriptors, layouts and the chosen algorithm). The first call of a
@@ -204,11 +206,19 @@ extern "C" void llmk_blas_destroy(llmk_blas* h) {
   delete h;
 }
 
+// Whether llmk_linear runs its own few-rows kernel (llmk_linear_rows) for this call.
+static bool rows_kernel_applies(const uint16_t* x, const uint16_t* w, int T, int in_features) {
+  return T <= LLMK_LINEAR_ROWS_MAX && in_features % 512 == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+}
+
 extern "C" int llmk_linear(llmk_blas* h, const uint16_t* x, const uint16_t* w, uint16_t* y, int T,
                            int in_features, int out_features, void* stream) {
   if (!h || T < 0 || in_features <= 0 || out_features <= 0) return LLMK_ERR_INVALID_VALUE;
   if (T == 0) return LLMK_OK;
   if (!x || !w || !y) return LLMK_ERR_INVALID_VALUE;
+  if (rows_kernel_applies(x, w, T, in_features))
+    return llmk_linear_rows(x, w, y, T, in_features, out_features, stream);
   Plan p;
   {
     std::lock_guard<std::mutex> lock(h->mu);
@@ -234,6 +244,7 @@ extern "C" int llmk_blas_tune(llmk_blas* h, const uint16_t* x, const uint16_t* w
                               int T, int in_features, int out_features, void* stream) {
   if (!h || T <= 0 || in_features <= 0 || out_features <= 0 || !x || !w || !y)
     return LLMK_ERR_INVALID_VALUE;
+  if (rows_kernel_applies(x, w, T, in_features)) return LLMK_OK;  // no library plan to choose
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap) != hipSuccess ||
       cap != hipStreamCaptureStatusNone)

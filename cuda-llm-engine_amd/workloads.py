@@ -140,6 +140,23 @@ def decode_step_rows(lens: np.ndarray, max_pages: int = 128, seed: int = SEED_BA
     return tokens, (lens - 1).astype(np.int32), tables, total
 
 
+# The reference's continuous-batching workload (ref: tests/test_scheduler.cu:15,35-40,
+# docs/scheduler_results.md): its 8 prompts (token counts from tests/reference/reference.json),
+# three times each, 32 new tokens per request, one request eligible every 2 scheduler
+# iterations, 256 pages of 16 positions, at most 8 sequences at once.
+SCHED_PROMPT_LENS = (6, 5, 5, 11, 12, 15, 12, 402)
+SCHED_REQUESTS, SCHED_NEW, SCHED_SPACING, SCHED_PAGES, SCHED_MAX_RUNNING = 24, 32, 2, 256, 8
+
+
+def scheduler_requests(seed: int = SEED_BASE + 11) -> list:
+    """The reference scheduler workload with seeded synthetic prompt ids (the weights are random,
+    so the prompts' text does not matter; their lengths set the prefill work)."""
+    rng = np.random.default_rng(seed)
+    prompts = [rng.integers(0, VOCAB, n).tolist() for n in SCHED_PROMPT_LENS]
+    return [{"id": i, "prompt": prompts[i % len(prompts)], "max_new": SCHED_NEW,
+             "arrival_step": i * SCHED_SPACING} for i in range(SCHED_REQUESTS)]
+
+
 def attention_lens(n: int = 256, max_len: int = 2048, seed: int = SEED_BASE + 6) -> np.ndarray:
     """Sequence lengths uniform in [1, max_len] (the decode configuration's context lengths)."""
     return np.random.default_rng(seed).integers(1, max_len + 1, n)

@@ -222,12 +222,24 @@ LLMK_API int llmk_blas_create(llmk_blas** out);
 LLMK_API void llmk_blas_destroy(llmk_blas* h);
 
 /* y[T, out_features] = x[T, in_features] * W^T, W stored [out_features, in_features] row-major
- * (a PyTorch Linear without bias); fp16 in and out, fp32 accumulation. The first call of a shape
- * takes hipBLASLt's heuristic choice (make that call outside graph capture); later calls only
- * enqueue. ref: kernels/linear.cuh:5-7, kernels/linear.cu:5-25 (linear; cublasHandle_t ->
- * llmk_blas*). */
+ * (a PyTorch Linear without bias); fp16 in and out, fp32 accumulation. With T <= 8,
+ * in_features % 512 == 0 and x, W 16-byte aligned it runs llmk_linear_rows; otherwise the first
+ * call of a shape takes hipBLASLt's heuristic choice (make that call outside graph capture) and
+ * later calls only enqueue. ref: kernels/linear.cuh:5-7, kernels/linear.cu:5-25 (linear;
+ * cublasHandle_t -> llmk_blas*). */
 LLMK_API int llmk_linear(llmk_blas* h, const uint16_t* x, const uint16_t* w, uint16_t* y, int T,
                          int in_features, int out_features, void* stream);
+
+/* The row limit of llmk_linear_rows. */
+#define LLMK_LINEAR_ROWS_MAX 8
+
+/* llmk_linear for a few rows (T <= LLMK_LINEAR_ROWS_MAX): a kernel of this library that streams
+ * W from HBM (a decode step with few sequences is a GEMV; its time is the weight read).
+ * in_features % 512 == 0; x and W 16-byte aligned; no handle, no workspace, allocates nothing.
+ * Sums run in another order than hipBLASLt's, so results agree to fp32 rounding. New entry
+ * point; the reference's linear (kernels/linear.cu:5-25) covers every T with cuBLAS. */
+LLMK_API int llmk_linear_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, int T,
+                              int in_features, int out_features, void* stream);
 
 /* Chooses the algorithm of one shape by timing hipBLASLt's heuristic candidates with cold
  * caches, on `stream` with these operands (y is overwritten; synchronous; not while the stream

@@ -68,6 +68,48 @@ def test_linear_matches_oracle(llmk, orc, blas, T, K, N):
     assert bad == 0 and exact > 0.9
 
 
+@pytest.mark.parametrize("K,N", [(2048, 3072), (2048, 2048), (8192, 2048), (512, 1000),
+                                 (2048, 16384), (1024, 13)])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8])
+def test_linear_rows_matches_oracle(llmk, orc, T, K, N):
+    """The few-rows kernel (T <= 8): every row count of each padded width (1, 2, 4, 8), output
+    widths that are not multiples of the kernel's 8 rows per block, and in_features over several
+    steps per wave (8192)."""
+    rng = np.random.default_rng(0x5EED0210 + 16 * T + K // 512)
+    x = normal_f16(rng, (T, K))
+    w = normal_f16(rng, (N, K), std=0.02)
+    y = torch.full((T * N + 64,), float("nan"), dtype=torch.float16, device=DEV)
+    print(f"linear_rows T={T} K={K} N={N}", flush=True)
+    llmk.linear_rows(dev(x), dev(w), y, T, K, N)
+    torch.cuda.synchronize()
+    got = host(y)
+    assert np.all(got[T * N:] == 0x7E00), "write past the output"
+    bad, exact = linear_rule(got[:T * N], orc.linear(x, w, T, K, N, threads=16).ravel())
+    print(f"  bad {bad} exact {100 * exact:.2f}%")
+    assert bad == 0 and exact > 0.9
+
+
+def test_linear_rows_preconditions(llmk, blas):
+    x = torch.zeros(9 * 512 + 8, dtype=torch.float16, device=DEV)
+    w = torch.zeros(16 * 512 + 8, dtype=torch.float16, device=DEV)
+    y = torch.zeros(9 * 16, dtype=torch.float16, device=DEV)
+    with pytest.raises(llmk.LlmkError, match="shape outside"):
+        llmk.linear_rows(x, w, y, 9, 512, 16)                    # more than 8 rows
+    with pytest.raises(llmk.LlmkError, match="shape outside"):
+        llmk.linear_rows(x, w, y, 2, 256, 16)                    # in_features % 512 != 0
+    with pytest.raises(llmk.LlmkError, match="aligned"):
+        llmk.linear_rows(x[1:], w, y, 2, 512, 16)                # x not 16-byte aligned
+    llmk.linear_rows(x, w, y, 0, 512, 16)                        # no rows: nothing to do
+    # llmk_linear takes the hipBLASLt path where the few-rows kernel does not apply
+    xs = normal_f16(np.random.default_rng(7), (2, 256))
+    ws = normal_f16(np.random.default_rng(8), (16, 256), std=0.02)
+    yy = torch.empty(32, dtype=torch.float16, device=DEV)
+    llmk.linear(blas, dev(xs), dev(ws), yy, 2, 256, 16)
+    torch.cuda.synchronize()
+    ref = (xs.view(np.float16).astype(np.float32) @ ws.view(np.float16).astype(np.float32).T).ravel()
+    assert np.allclose(host(yy).view(np.float16).astype(np.float32), ref, atol=2e-2, rtol=2e-2)
+
+
 def test_linear_after_tuning_matches_oracle(llmk, orc, blas):
     """llmk_blas_tune swaps a shape's algorithm for the fastest timed candidate; the result
     keeps the same bar."""
