@@ -215,3 +215,25 @@ def test_a_model_error_ends_the_run_and_returns_the_pages(llmk):
     with pytest.raises(ValueError):
         llmk.run_scheduler(reqs, 3, 4, P, pages, llmk.python_sched_model(prefill, decode))
     assert pages.num_free() == 16
+
+
+@pytest.mark.parametrize("max_running,steps", [(1, 744), (8, 107)])
+def test_the_reference_workload_gives_its_published_schedule(llmk, max_running, steps):
+    """The reference's scheduler benchmark (ref: tests/test_scheduler.cu:15,35-40): its 8 prompt
+    lengths three times, 32 new tokens each, one request every 2 iterations, 256 pages. The
+    reference publishes 744 decode steps one at a time and 107 with up to 8 at once, mean batch
+    7.0 (docs/scheduler_results.md); the schedule depends only on the lengths and the rules, so
+    this scheduler must reproduce both counts."""
+    import importlib
+    wl = importlib.import_module("llmk.workloads")
+    reqs = wl.scheduler_requests()
+    assert [len(r["prompt"]) for r in reqs[:8]] == [6, 5, 5, 11, 12, 15, 12, 402]
+    max_pages = (max(len(r["prompt"]) for r in reqs) + wl.SCHED_NEW + P - 1) // P
+    outs, stats, _, fake, pages = run_cpp(llmk, reqs, max_running, wl.SCHED_PAGES, max_pages)
+    assert stats["decode_steps"] == steps
+    assert stats["total_words"] == 24 * 32
+    assert round(stats["mean_batch"], 1) == (1.0 if max_running == 1 else 7.0)
+    assert pages.num_free() == wl.SCHED_PAGES
+    assert outs == [expected_outputs(r["prompt"], r["max_new"]) for r in reqs]
+    o_outs, o_stats, _, _ = run_oracle(reqs, max_running, wl.SCHED_PAGES, max_pages)
+    assert o_stats["decode_steps"] == steps and o_outs == outs
