@@ -152,6 +152,12 @@ _SIGS = {
     "llmk_blas_destroy": (None, [_vp]),
     "llmk_linear": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "llmk_linear_rows": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "llmk_linear_rows_norm": (_i, [_vp, _vp, _f, _vp, _vp, _i, _i, _i, _vp]),
+    "llmk_engine_set_option": (_i, [_vp, _i, _i]),
+    "llmk_linear_rows_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "llmk_linear_rows_swiglu": (_i, [_vp, _vp, _f, _vp, _vp, _i, _i, _i, _vp]),
+    "llmk_linear_rows_qkv_rope_scatter": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                               _i, _i, _i, _i, _i, _vp]),
     "llmk_qkv_rope_scatter": (_i, [_vp, _i] + [_vp] * 6 + [_i] * 6 + [_vp]),
     "llmk_swiglu_rows": (_i, [_vp, _vp, _i, _i, _vp]),
     "llmk_engine_create": (_i, [ctypes.POINTER(ModelConfig), _i, _i, _i, ctypes.POINTER(_vp)]),
@@ -560,6 +566,7 @@ def linear(handle: Blas, x, w, y, T: int, in_features: int, out_features: int,
 
 
 LINEAR_ROWS_MAX = 8  # LLMK_LINEAR_ROWS_MAX
+ENGINE_FUSE_FEW_ROWS = 1  # LLMK_ENGINE_FUSE_FEW_ROWS
 
 
 def linear_rows(x, w, y, T: int, in_features: int, out_features: int, stream=None) -> None:
@@ -572,6 +579,65 @@ def linear_rows(x, w, y, T: int, in_features: int, out_features: int, stream=Non
     pw = _dev(fn, w, torch.float16, out_features * in_features, "w")
     py = _dev(fn, y, torch.float16, T * out_features, "y")
     _check(fn, _lib.llmk_linear_rows(px, pw, py, T, in_features, out_features, _stream(stream)))
+
+
+def _norm_ptr(fn, norm_w, in_features):
+    return None if norm_w is None else _dev(fn, norm_w, torch.float16, in_features, "norm_w")
+
+
+def linear_rows_norm(x, norm_w, eps: float, w, y, T: int, in_features: int, out_features: int,
+                     stream=None) -> None:
+    """y = rmsnorm(x) W^T for T <= 8 rows; norm_w None: y = x W^T (``llmk_linear_rows_norm``)."""
+    fn = "linear_rows_norm"
+    px = _dev(fn, x, torch.float16, T * in_features, "x")
+    pw = _dev(fn, w, torch.float16, out_features * in_features, "w")
+    py = _dev(fn, y, torch.float16, T * out_features, "y")
+    _check(fn, _lib.llmk_linear_rows_norm(px, _norm_ptr(fn, norm_w, in_features), eps, pw, py, T,
+                                          in_features, out_features, _stream(stream)))
+
+
+def linear_rows_residual(x, w, residual, T: int, in_features: int, out_features: int,
+                         stream=None) -> None:
+    """residual += x W^T, rounded as linear then residual_add (``llmk_linear_rows_residual``)."""
+    fn = "linear_rows_residual"
+    px = _dev(fn, x, torch.float16, T * in_features, "x")
+    pw = _dev(fn, w, torch.float16, out_features * in_features, "w")
+    pr = _dev(fn, residual, torch.float16, T * out_features, "residual")
+    _check(fn, _lib.llmk_linear_rows_residual(px, pw, pr, T, in_features, out_features,
+                                              _stream(stream)))
+
+
+def linear_rows_swiglu(x, norm_w, eps: float, w_gate_up, act, T: int, in_features: int,
+                       inter: int, stream=None) -> None:
+    """act = swiglu of the gate and up projections of rmsnorm(x) (``llmk_linear_rows_swiglu``)."""
+    fn = "linear_rows_swiglu"
+    px = _dev(fn, x, torch.float16, T * in_features, "x")
+    pw = _dev(fn, w_gate_up, torch.float16, 2 * inter * in_features, "w_gate_up")
+    pa = _dev(fn, act, torch.float16, T * inter, "act")
+    _check(fn, _lib.llmk_linear_rows_swiglu(px, _norm_ptr(fn, norm_w, in_features), eps, pw, pa,
+                                            T, in_features, inter, _stream(stream)))
+
+
+def linear_rows_qkv_rope_scatter(x, norm_w, eps: float, w_qkv, q_out, k_pool, v_pool,
+                                 block_tables, positions, inv_freq, T: int, in_features: int,
+                                 n_heads: int, n_kv_heads: int, max_pages: int,
+                                 stream=None) -> None:
+    """The QKV projection of rmsnorm(x) with RoPE and the KV scatter in its epilogue (head_dim
+    64, page size 16; ``llmk_linear_rows_qkv_rope_scatter``). The tables and positions are not
+    checked against the pools here; the caller owns that."""
+    fn = "linear_rows_qkv_rope_scatter"
+    out = (n_heads + 2 * n_kv_heads) * 64
+    px = _dev(fn, x, torch.float16, T * in_features, "x")
+    pw = _dev(fn, w_qkv, torch.float16, out * in_features, "w_qkv")
+    pq = _dev(fn, q_out, torch.float16, T * n_heads * 64, "q_out")
+    pk = _dev(fn, k_pool, torch.float16, n_kv_heads * 64, "k_pool")
+    pv = _dev(fn, v_pool, torch.float16, n_kv_heads * 64, "v_pool")
+    pt = _dev(fn, block_tables, torch.int32, T * max_pages, "block_tables")
+    pp = _dev(fn, positions, torch.int32, T, "positions")
+    pf = _dev(fn, inv_freq, torch.float32, 32, "inv_freq")
+    _check(fn, _lib.llmk_linear_rows_qkv_rope_scatter(
+        px, _norm_ptr(fn, norm_w, in_features), eps, pw, pq, pk, pv, pt, pp, pf, T, in_features,
+        n_heads, n_kv_heads, max_pages, _stream(stream)))
 
 
 def blas_tune(handle: Blas, x, w, y, T: int, in_features: int, out_features: int,
@@ -744,6 +810,10 @@ class Engine:
 
     def reset_pools(self, stream=None) -> None:
         _check("engine_reset_pools", _lib.llmk_engine_reset_pools(self._e, _stream(stream)))
+
+    def set_option(self, option: int, value: int) -> None:
+        """``llmk_engine_set_option`` (ENGINE_FUSE_FEW_ROWS)."""
+        _check("engine_set_option", _lib.llmk_engine_set_option(self._e, option, value))
 
     def buffer_ptr(self, which: int, layer: int = 0) -> int:
         p = _lib.llmk_engine_buffer(self._e, which, layer)

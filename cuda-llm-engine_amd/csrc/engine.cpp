@@ -95,6 +95,7 @@ struct llmk_engine {
   };
   std::map<std::tuple<int, int, int>, Graph> graphs;
   hipStream_t sched_stream = nullptr;  // the stream the scheduler callbacks run on
+  bool fuse_rows = true;  // passes of <= LLMK_LINEAR_ROWS_MAX rows use the fused projections
 };
 
 namespace {
@@ -421,6 +422,69 @@ extern "C" int llmk_engine_set_rows(llmk_engine* e, int n_rows, const int32_t* t
   return st;
 }
 
+// Whether a pass over n rows takes the fused few-rows path: every projection is a
+// llmk_linear_rows_* call with the norms, RoPE + scatter, SwiGLU and residual adds in its
+// prologue or epilogue (5 + 1 launches per layer instead of 9 + 1).
+static bool fused_rows_path(const llmk_engine* e, int n) {
+  const llmk_model_config& m = e->cfg;
+  if (!e->fuse_rows || n > LLMK_LINEAR_ROWS_MAX) return false;
+  const int steps = m.hidden / 512;  // the norm prologue: one 512-wide step per wave
+  return m.hidden % 512 == 0 && e->qdim % 512 == 0 && m.inter % 512 == 0 && m.head_dim == 64 &&
+         (steps & (steps - 1)) == 0 && steps <= (n > 4 ? 8 : 16);
+}
+
+static int forward_fused_rows(llmk_engine* e, int n, int nl, bool all_rows, int num_splits,
+                              void* s) {
+  const llmk_model_config& m = e->cfg;
+  const int H = m.hidden, L = m.n_layers;
+#define LLMK_TRY(call)               \
+  do {                               \
+    const int st_ = (call);          \
+    if (st_ != LLMK_OK) return st_;  \
+  } while (0)
+  LLMK_TRY(llmk_embedding_lookup(e->embed, e->tokens, e->x, n, H, s));
+  for (int l = 0; l < L; ++l) {
+    const LayerPtrs& w = e->layers[l];
+    LLMK_TRY(llmk_linear_rows_qkv_rope_scatter(
+        e->x, w.attn_norm, m.eps, w.wqkv, e->q, e->k_pool[l], e->v_pool[l], e->tables,
+        e->positions, e->inv_freq, n, H, m.n_heads, m.n_kv_heads, e->max_pages, s));
+    LLMK_TRY(llmk_attention_decode_fast(e->q, e->k_pool[l], e->v_pool[l], e->tables, e->lens,
+                                        e->attn, e->ws, n, e->max_pages, kPage, m.n_heads,
+                                        m.n_kv_heads, m.head_dim, num_splits, s));
+    LLMK_TRY(llmk_linear_rows_residual(e->attn, w.wo, e->x, n, e->qdim, H, s));
+    LLMK_TRY(llmk_linear_rows_swiglu(e->x, w.mlp_norm, m.eps, w.wgu, e->act, n, H, m.inter, s));
+    LLMK_TRY(llmk_linear_rows_residual(e->act, w.wdown, e->x, n, m.inter, H, s));
+  }
+  const uint16_t* lm_in = e->x;
+  if (!all_rows) {
+    if (nl == 0) return LLMK_OK;
+    LLMK_TRY(llmk_embedding_lookup(e->x, e->logit_rows, e->fin, nl, H, s));
+    lm_in = e->fin;
+  }
+  LLMK_TRY(llmk_linear_rows_norm(lm_in, e->final_norm, m.eps, e->embed, e->logits, nl, H,
+                                 m.vocab, s));
+  LLMK_TRY(llmk_argmax_rows(e->logits, e->next, nl, m.vocab, s));
+#undef LLMK_TRY
+  return LLMK_OK;
+}
+
+extern "C" int llmk_engine_set_option(llmk_engine* e, int option, int value) {
+  if (!e) return LLMK_ERR_INVALID_VALUE;
+  switch (option) {
+    case LLMK_ENGINE_FUSE_FEW_ROWS:
+      if (e->fuse_rows != (value != 0)) {
+        // cached graphs hold the other path
+        for (auto& kv : e->graphs)
+          if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+        e->graphs.clear();
+      }
+      e->fuse_rows = value != 0;
+      return LLMK_OK;
+    default:
+      return LLMK_ERR_INVALID_VALUE;
+  }
+}
+
 extern "C" int llmk_engine_forward(llmk_engine* e, int n_rows, int n_logit_rows, int num_splits,
                                    void* stream) {
   if (!e || n_rows < 0 || n_rows > e->max_rows || n_logit_rows > n_rows)
@@ -439,6 +503,7 @@ extern "C" int llmk_engine_forward(llmk_engine* e, int n_rows, int n_logit_rows,
   }
   if (num_splits > kMaxSplits) num_splits = kMaxSplits;
   void* s = stream;
+  if (fused_rows_path(e, n)) return forward_fused_rows(e, n, nl, all_rows, num_splits, s);
 #define LLMK_TRY(call)               \
   do {                               \
     const int st_ = (call);          \

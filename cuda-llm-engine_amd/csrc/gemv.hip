@@ -5,12 +5,14 @@
 //
 // With T <= 8 rows a projection does at most 16 flops per weight byte, far below MI355X's ~300
 // flop/byte balance point, so it is a stream over W: the design goal is to keep HBM busy.
-//   - A block owns kRows = 8 consecutive output rows. The in dimension is cut into steps of 512
-//     (64 lanes x 8 halves), and the block's WV waves (4, 8 or 16: one step each where the
-//     registers allow) take steps w, w + WV, ... For each step a wave issues one 16-byte load per
-//     W row (64 lanes cover 1 KiB of the row, fully coalesced) and one per x row (x is small and
-//     stays in the L2), then accumulates the 8 x T partial dot products of its lane in fp32 with
+//   - A block owns kRows = 8 output rows. The in dimension is cut into steps of 512 (64 lanes x
+//     8 halves), and the block's WV waves (1 to 16: one step each where the registers allow)
+//     take steps w, w + WV, ... For each step a wave issues one 16-byte load per W row (64 lanes
+//     cover 1 KiB of the row, fully coalesced) and one per x row (x is small and stays in the
+//     L2), then accumulates the 8 x T partial dot products of its lane in fp32 with
 //     v_dot2_f32_f16.
+//   - Fused variants (the entry points at the end) normalise x on the fly and replace the store
+//     with the residual add, SwiGLU, or RoPE + KV scatter of the decode step.
 //   - The 8 * TP partial sums of a lane are then reduced over the wave in a halving butterfly:
 //     at each exchange a lane keeps half of its values and adds its partner's copy of them, so
 //     the 64 lanes end up holding distinct (row, token) sums after 63 adds (mostly DPP) instead
@@ -18,6 +20,7 @@
 // Summation order differs from cuBLAS/hipBLASLt (lane-strided partial sums, then the butterfly),
 // so results agree with the fp32 dot product to fp32 rounding, not bit for bit.
 #include "common.hpp"
+#include "pointwise.hpp"
 
 namespace llmk {
 namespace {
@@ -98,17 +101,62 @@ __device__ __forceinline__ int butterfly_index(int lane, bool* writer) {
   return idx;
 }
 
+// What a launch computes besides the plain product. See the entry points at the end of the file.
+enum Epi : int {
+  kEpiStore = 0,     // y[t][j] = r16(sum)
+  kEpiResidual = 1,  // y[t][j] = r16(y[t][j] + r16(sum)), in place (the residual add)
+  kEpiSwiglu = 2,    // rows j (gate) and inter + j (up) -> y[t][j] = r16(r16(silu(g)) * u)
+  kEpiRope = 3,      // rows of q, k, v heads: RoPE on q and k, k and v into the paged pools
+};
+
+struct RowsArgs {
+  const f16* x;       // [T, in]; with norm_w, the rows are normalised first (RMSNorm)
+  const f16* w;       // [out, in] row-major
+  f16* y;             // see Epi
+  int T, in, out;
+  const f16* norm_w;  // [in] or null
+  float eps;
+  // kEpiRope: out = (n_heads + 2 n_kv_heads) * 64 rows: q heads, k heads, v heads
+  f16* q_out;         // [T, n_heads, 64]
+  f16* k_pool;        // [num_pages * 16, n_kv_heads * 64]
+  f16* v_pool;
+  const int* tables;  // [T, max_pages]
+  const int* positions;
+  const float* inv_freq;  // [32]
+  int n_heads, n_kv_heads, max_pages;
+};
+
+// Output row r (0..7) of block b. The swiglu and rope blocks take pairs: rows r and r + 4 are a
+// (gate, up) pair of the same column, or the two halves (i, i + 32) of a rotation pair.
+template <int EPI>
+__device__ __forceinline__ int row_of(int b, int r, const RowsArgs& a) {
+  if constexpr (EPI == kEpiSwiglu) {
+    const int j = 4 * b + (r & 3);
+    return r < 4 ? j : a.out / 2 + j;
+  } else if constexpr (EPI == kEpiRope) {
+    const int h = b >> 3, i = 4 * (b & 7) + (r & 3);
+    return h * 64 + (r < 4 ? i : 32 + i);
+  } else {
+    const int j = b * kRows + r;
+    return j < a.out ? j : a.out - 1;  // rows past `out`: computed, not stored
+  }
+}
+
 // TP: rows computed (a power of two >= T; rows t >= T reuse row T - 1 and are not stored).
 // WV: waves per block, dividing the in dimension's steps between them.
-template <int TP, int WV>
-__global__ void __launch_bounds__(64 * WV)
-k_gemv(const f16* __restrict__ x, const f16* __restrict__ w, f16* __restrict__ y, int T, int in,
-       int out) {
+// NORM: x is RMSNorm-ed on the fly; the launcher then gives every wave exactly one step
+// (steps == WV). Each row's sum of squares is taken exactly as the RMSNorm kernel takes it
+// (k_rmsnorm_wave: lane l sums elements 8 (l + 64 k) + j, k then j in order, then wave_sum), by
+// wave t % WV, so the normalised values are the RMSNorm kernel's bits.
+template <int TP, int WV, int EPI, bool NORM>
+__global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
   constexpr int N = kRows * TP;  // partial sums per lane: value index r * TP + t
   __shared__ float part[WV][N];
+  __shared__ float inv_s[TP];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int j0 = blockIdx.x * kRows;
+  const int b = blockIdx.x;
+  const int in = a.in, T = a.T;
   const int steps = in / kStep;
 
   float v[64];
@@ -116,28 +164,77 @@ k_gemv(const f16* __restrict__ x, const f16* __restrict__ w, f16* __restrict__ y
   for (int i = 0; i < 64; ++i) v[i] = 0.0f;
   const f16* wr[kRows];
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const int j = j0 + r < out ? j0 + r : out - 1;  // rows past `out`: computed, not stored
-    wr[r] = w + (size_t)j * in + lane * 8;
-  }
+  for (int r = 0; r < kRows; ++r) wr[r] = a.w + (size_t)row_of<EPI>(b, r, a) * in + lane * 8;
   const f16* xr[TP];
 #pragma unroll
-  for (int t = 0; t < TP; ++t) xr[t] = x + (size_t)(t < T ? t : T - 1) * in + lane * 8;
+  for (int t = 0; t < TP; ++t) xr[t] = a.x + (size_t)(t < T ? t : T - 1) * in + lane * 8;
 
-  for (int s = wave; s < steps; s += WV) {
-    const size_t k = (size_t)s * kStep;
+  if constexpr (NORM) {
+    // The rows whose norms this wave takes (t = wave + WV q), loaded first so that waiting for
+    // them does not wait for the W loads issued after them.
+    constexpr int NQ = (TP + WV - 1) / WV;
+    u32x4 nr[NQ][WV];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int t = (wave + WV * q) % TP;  // waves past the last row repeat one (not stored)
+      const f16* row = a.x + (size_t)(t < T ? t : T - 1) * in + lane * 8;
+#pragma unroll
+      for (int k = 0; k < WV; ++k) nr[q][k] = ld16(row + (size_t)k * kStep);
+    }
+    const size_t k0 = (size_t)wave * kStep;  // this wave's one step
     u32x4 wv[kRows], xv[TP];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) wv[r] = ld16_stream(wr[r] + k);
+    for (int r = 0; r < kRows; ++r) wv[r] = ld16_stream(wr[r] + k0);
 #pragma unroll
-    for (int t = 0; t < TP; ++t) xv[t] = ld16(xr[t] + k);
-    // Every load of the step is in flight before the first product (left alone, the scheduler
-    // reuses one register for the W rows and waits for each load in turn).
+    for (int t = 0; t < TP; ++t) xv[t] = ld16(xr[t] + k0);
+    const u32x4 nw = ld16(a.norm_w + k0 + lane * 8);
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < WV; ++k) {
+        const f16x8 h = as_h8(nr[q][k]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float f = (float)h[j];
+          ss = ss + f * f;
+        }
+      }
+      ss = wave_sum(ss);
+      const int t = wave + WV * q;
+      if (lane == 0 && t < TP) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TP; ++t) {
+      const f16x8 h = as_h8(xv[t]);
+      const float inv = inv_s[t];
+      f16x8 an;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
+      xv[t] = as_u4(as_h8(nw) * an);
+    }
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
 #pragma unroll
       for (int t = 0; t < TP; ++t) v[r * TP + t] = dot8(wv[r], xv[t], v[r * TP + t]);
+  } else {
+    for (int s = wave; s < steps; s += WV) {
+      const size_t k = (size_t)s * kStep;
+      u32x4 wv[kRows], xv[TP];
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) wv[r] = ld16_stream(wr[r] + k);
+#pragma unroll
+      for (int t = 0; t < TP; ++t) xv[t] = ld16(xr[t] + k);
+      // Every load of the step is in flight before the first product (left alone, the
+      // scheduler reuses one register for the W rows and waits for each load in turn).
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < kRows; ++r)
+#pragma unroll
+        for (int t = 0; t < TP; ++t) v[r * TP + t] = dot8(wv[r], xv[t], v[r * TP + t]);
+    }
   }
 
   butterfly<N, 0>(v);
@@ -145,25 +242,119 @@ k_gemv(const f16* __restrict__ x, const f16* __restrict__ w, f16* __restrict__ y
   const int idx = butterfly_index<N>(lane, &writer);
   if (writer) part[wave][idx] = v[0];
   __syncthreads();
-  if (threadIdx.x < N) {
-    const int r = threadIdx.x / TP, t = threadIdx.x % TP;
+  auto total = [&](int i) {
     float sum = 0.0f;
 #pragma unroll
-    for (int q = 0; q < WV; ++q) sum += part[q][threadIdx.x];
-    if (j0 + r < out && t < T) y[(size_t)t * out + j0 + r] = (f16)sum;
+    for (int q = 0; q < WV; ++q) sum += part[q][i];
+    return sum;
+  };
+  const int tid = threadIdx.x;
+  if constexpr (EPI == kEpiStore || EPI == kEpiResidual) {
+    if (tid < N) {
+      const int r = tid / TP, t = tid % TP, j = b * kRows + r;
+      if (j < a.out && t < T) {
+        const f16 p = (f16)total(tid);
+        f16* dst = a.y + (size_t)t * a.out + j;
+        *dst = EPI == kEpiStore ? p : (f16)((float)*dst + (float)p);
+      }
+    }
+  } else if (tid < 4 * TP) {
+    const int r = tid / TP, t = tid % TP;  // the pair (r, r + 4) of token t
+    if (t < T) {
+      const f16 lo = (f16)total(tid), hi = (f16)total(tid + 4 * TP);
+      if constexpr (EPI == kEpiSwiglu) {
+        const int inter = a.out / 2, j = 4 * b + r;
+        a.y[(size_t)t * inter + j] = silu_r16(lo) * hi;
+      } else {
+        const int h = b >> 3, i = 4 * (b & 7) + r, nq = a.n_heads, nkv = a.n_kv_heads;
+        const int pos = a.positions[t];
+        f16 x1 = lo, x2 = hi;
+        if (h < nq + nkv) {
+          f16 c, sn;
+          cos_sin_f16((float)pos * a.inv_freq[i], &c, &sn);
+          x1 = lo * c - hi * sn;
+          x2 = hi * c + lo * sn;
+        }
+        f16* dst;
+        if (h < nq) {
+          dst = a.q_out + ((size_t)t * nq + h) * 64;
+        } else {
+          const size_t prow = (size_t)a.tables[(size_t)t * a.max_pages + pos / 16] * 16 + pos % 16;
+          const int hk = h < nq + nkv ? h - nq : h - nq - nkv;
+          dst = (h < nq + nkv ? a.k_pool : a.v_pool) + prow * nkv * 64 + hk * 64;
+        }
+        dst[i] = x1;
+        dst[i + 32] = x2;
+      }
+    }
   }
 }
 
-// Waves per block: enough that a wave takes one step of the in dimension, up to 16 (8 with 8
-// rows, whose 130 registers a 1024-thread block cannot give every wave).
+// Waves per block: one per step of the in dimension, up to 16 (8 with 8 rows, whose 130
+// registers a 1024-thread block cannot give every wave). A normalising launch needs exactly one
+// step per wave, so steps must be 1, 2, 4, 8 or 16 (at most 8 with 8 rows); 0 otherwise.
 template <int TP>
-int gemv_launch(const f16* x, const f16* w, f16* y, int T, int in, int out, hipStream_t s) {
-  const dim3 grid(ceil_div((size_t)out, kRows));
-  const int steps = in / kStep;
-  if constexpr (TP < 8)
-    if (steps > 8) return launch(k_gemv<TP, 16>, grid, dim3(64 * 16), 0, s, x, w, y, T, in, out);
-  if (steps > 4) return launch(k_gemv<TP, 8>, grid, dim3(64 * 8), 0, s, x, w, y, T, in, out);
-  return launch(k_gemv<TP, 4>, grid, dim3(64 * 4), 0, s, x, w, y, T, in, out);
+int rows_waves(int steps, bool norm) {
+  const int cap = TP < 8 ? 16 : 8;
+  if (norm) {
+    const bool pow2 = (steps & (steps - 1)) == 0;
+    return steps >= 1 && steps <= cap && pow2 ? steps : 0;
+  }
+  return steps <= 1 ? 1 : steps <= 2 ? 2 : steps <= 4 ? 4 : steps <= 8 ? 8 : cap;
+}
+
+template <int TP, int EPI, bool NORM>
+int rows_launch_tp(const RowsArgs& a, unsigned blocks, hipStream_t s) {
+  const int wv = rows_waves<TP>(a.in / kStep, NORM);
+  switch (wv) {
+    case 1: return launch(k_rows<TP, 1, EPI, NORM>, dim3(blocks), dim3(64), 0, s, a);
+    case 2: return launch(k_rows<TP, 2, EPI, NORM>, dim3(blocks), dim3(128), 0, s, a);
+    case 4: return launch(k_rows<TP, 4, EPI, NORM>, dim3(blocks), dim3(256), 0, s, a);
+    case 8: return launch(k_rows<TP, 8, EPI, NORM>, dim3(blocks), dim3(512), 0, s, a);
+    case 16:
+      if constexpr (TP < 8) return launch(k_rows<TP, 16, EPI, NORM>, dim3(blocks), dim3(1024), 0, s, a);
+      return LLMK_ERR_UNSUPPORTED;
+    default: return LLMK_ERR_UNSUPPORTED;
+  }
+}
+
+template <int EPI, bool NORM>
+int rows_launch(const RowsArgs& a, unsigned blocks, hipStream_t s) {
+  if (a.T == 1) return rows_launch_tp<1, EPI, NORM>(a, blocks, s);
+  if (a.T == 2) return rows_launch_tp<2, EPI, NORM>(a, blocks, s);
+  if (a.T <= 4) return rows_launch_tp<4, EPI, NORM>(a, blocks, s);
+  return rows_launch_tp<8, EPI, NORM>(a, blocks, s);
+}
+
+template <int EPI>
+int rows_dispatch(const RowsArgs& a, unsigned blocks, hipStream_t s) {
+  return a.norm_w ? rows_launch<EPI, true>(a, blocks, s) : rows_launch<EPI, false>(a, blocks, s);
+}
+
+// Checks shared by the entry points; fills the common fields.
+int rows_common(RowsArgs* a, const uint16_t* x, const uint16_t* norm_w, float eps,
+                const uint16_t* w, uint16_t* y, int T, int in, int out) {
+  if (T < 0 || in <= 0 || out <= 0) return LLMK_ERR_INVALID_VALUE;
+  if (T > 0 && (!x || !w || !y)) return LLMK_ERR_INVALID_VALUE;
+  if (T > LLMK_LINEAR_ROWS_MAX || in % kStep != 0) return LLMK_ERR_UNSUPPORTED;
+  if ((size_t)out > (size_t)0xFFFFFFFFu * kRows) return LLMK_ERR_UNSUPPORTED;
+  if (norm_w) {
+    const int steps = in / kStep;
+    const int wv = T > 4 ? rows_waves<8>(steps, true) : rows_waves<4>(steps, true);
+    if (wv == 0) return LLMK_ERR_UNSUPPORTED;
+    if (!aligned16(norm_w)) return LLMK_ERR_ALIGNMENT;
+  }
+  if (T > 0 && (!aligned16(x) || !aligned16(w))) return LLMK_ERR_ALIGNMENT;
+  *a = RowsArgs{};
+  a->x = reinterpret_cast<const f16*>(x);
+  a->w = reinterpret_cast<const f16*>(w);
+  a->y = reinterpret_cast<f16*>(y);
+  a->T = T;
+  a->in = in;
+  a->out = out;
+  a->norm_w = reinterpret_cast<const f16*>(norm_w);
+  a->eps = eps;
+  return LLMK_OK;
 }
 
 }  // namespace
@@ -173,18 +364,60 @@ using namespace llmk;
 
 extern "C" int llmk_linear_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, int T,
                                 int in_features, int out_features, void* stream) {
-  if (T < 0 || in_features <= 0 || out_features <= 0) return LLMK_ERR_INVALID_VALUE;
-  if (T == 0) return LLMK_OK;
-  if (!x || !w || !y) return LLMK_ERR_INVALID_VALUE;
-  if (T > LLMK_LINEAR_ROWS_MAX || in_features % kStep != 0) return LLMK_ERR_UNSUPPORTED;
-  if (!aligned16(x) || !aligned16(w)) return LLMK_ERR_ALIGNMENT;
-  if ((size_t)out_features > (size_t)0xFFFFFFFFu * kRows) return LLMK_ERR_UNSUPPORTED;
-  const f16* xh = reinterpret_cast<const f16*>(x);
-  const f16* wh = reinterpret_cast<const f16*>(w);
-  f16* yh = reinterpret_cast<f16*>(y);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (T == 1) return gemv_launch<1>(xh, wh, yh, T, in_features, out_features, s);
-  if (T == 2) return gemv_launch<2>(xh, wh, yh, T, in_features, out_features, s);
-  if (T <= 4) return gemv_launch<4>(xh, wh, yh, T, in_features, out_features, s);
-  return gemv_launch<8>(xh, wh, yh, T, in_features, out_features, s);
+  return llmk_linear_rows_norm(x, nullptr, 0.0f, w, y, T, in_features, out_features, stream);
+}
+
+extern "C" int llmk_linear_rows_norm(const uint16_t* x, const uint16_t* norm_w, float eps,
+                                     const uint16_t* w, uint16_t* y, int T, int in_features,
+                                     int out_features, void* stream) {
+  RowsArgs a;
+  const int st = rows_common(&a, x, norm_w, eps, w, y, T, in_features, out_features);
+  if (st != LLMK_OK || T == 0) return st;
+  return rows_dispatch<kEpiStore>(a, ceil_div((size_t)out_features, kRows),
+                                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int llmk_linear_rows_residual(const uint16_t* x, const uint16_t* w,
+                                         uint16_t* residual, int T, int in_features,
+                                         int out_features, void* stream) {
+  RowsArgs a;
+  const int st = rows_common(&a, x, nullptr, 0.0f, w, residual, T, in_features, out_features);
+  if (st != LLMK_OK || T == 0) return st;
+  return rows_dispatch<kEpiResidual>(a, ceil_div((size_t)out_features, kRows),
+                                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int llmk_linear_rows_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps,
+                                       const uint16_t* w_gate_up, uint16_t* act, int T,
+                                       int in_features, int inter, void* stream) {
+  if (inter <= 0 || inter % 4 != 0) return inter <= 0 ? LLMK_ERR_INVALID_VALUE
+                                                      : LLMK_ERR_UNSUPPORTED;
+  RowsArgs a;
+  const int st = rows_common(&a, x, norm_w, eps, w_gate_up, act, T, in_features, 2 * inter);
+  if (st != LLMK_OK || T == 0) return st;
+  return rows_dispatch<kEpiSwiglu>(a, (unsigned)(inter / 4), static_cast<hipStream_t>(stream));
+}
+
+extern "C" int llmk_linear_rows_qkv_rope_scatter(
+    const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* w_qkv,
+    uint16_t* q_out, uint16_t* k_pool, uint16_t* v_pool, const int32_t* block_tables,
+    const int32_t* positions, const float* inv_freq, int T, int in_features, int n_heads,
+    int n_kv_heads, int max_pages, void* stream) {
+  if (n_heads <= 0 || n_kv_heads <= 0 || max_pages <= 0) return LLMK_ERR_INVALID_VALUE;
+  if (T > 0 && (!q_out || !k_pool || !v_pool || !block_tables || !positions || !inv_freq))
+    return LLMK_ERR_INVALID_VALUE;
+  RowsArgs a;
+  const int out = (n_heads + 2 * n_kv_heads) * 64;
+  const int st = rows_common(&a, x, norm_w, eps, w_qkv, q_out, T, in_features, out);
+  if (st != LLMK_OK || T == 0) return st;
+  a.q_out = reinterpret_cast<f16*>(q_out);
+  a.k_pool = reinterpret_cast<f16*>(k_pool);
+  a.v_pool = reinterpret_cast<f16*>(v_pool);
+  a.tables = block_tables;
+  a.positions = positions;
+  a.inv_freq = inv_freq;
+  a.n_heads = n_heads;
+  a.n_kv_heads = n_kv_heads;
+  a.max_pages = max_pages;
+  return rows_dispatch<kEpiRope>(a, (unsigned)(out / kRows), static_cast<hipStream_t>(stream));
 }

@@ -20,6 +20,7 @@
 #include <math.h>
 
 #include "common.hpp"
+#include "pointwise.hpp"
 
 namespace llmk {
 
@@ -35,20 +36,6 @@ static FastDiv make_fastdiv(uint32_t d) {
 }
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
   return (__umulhi(n, f.m) + n) >> f.s;
-}
-
-// cos and sin of the fp32 angle `a`, rounded to fp16. They are evaluated in fp64 (OCML sincos,
-// full-range argument reduction) and rounded fp64 -> fp32 -> fp16, so the fp16 values are the
-// roundings of the fp32 roundings of the exact results except in vanishingly rare ties. The
-// angles reach 131071 rad; an fp32 sincos with a last-bit error can move c or s by one fp16 ulp,
-// and x1*c - x2*s then cancels to a value with a large relative error. 32 evaluations per
-// token, shared by all of its heads, keep the fp64 cost off the critical path.
-__device__ __forceinline__ void cos_sin_f16(float a, f16* c, f16* s) {
-  double sd, cd;
-  sincos((double)a, &sd, &cd);
-  const float cf = (float)cd, sf = (float)sd;
-  *c = (f16)cf;
-  *s = (f16)sf;
 }
 
 // The 16 bytes held by lane (lane ^ HV) of the same wave. HV < 16 stays inside a 16-lane DPP

@@ -241,6 +241,39 @@ LLMK_API int llmk_linear(llmk_blas* h, const uint16_t* x, const uint16_t* w, uin
 LLMK_API int llmk_linear_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, int T,
                               int in_features, int out_features, void* stream);
 
+/* The few-rows projection with the decode step's neighbouring element-wise work done in the same
+ * kernel (T <= LLMK_LINEAR_ROWS_MAX, in_features % 512 == 0, 16-byte aligned operands). With
+ * norm_w non-null the x rows are first RMSNorm-ed with weight norm_w [in_features] and eps,
+ * giving the bits llmk_rmsnorm gives (in_features / 512 a power of two up to 16, or up to 8
+ * with T > 4); with
+ * norm_w null x is used as is. Each epilogue rounds the projection to fp16 first and then
+ * applies the reference's formula, so every result has the bits of llmk_linear_rows followed
+ * by the separate launch. New entry points, for the engine's decode steps with few sequences;
+ * they replace ref: engine/batched.cu:51-58 (rmsnorm, three projections, rope_apply, two
+ * kv_scatter_batch), :62-64 (o projection, residual_add), :66-69 (rmsnorm, gate and up
+ * projections, swiglu) and :70-71 (down projection, residual_add).
+ *   _norm: y[T, out] = norm(x) W^T.
+ *   _residual: residual[T, out] = fp16(residual + fp16(x W^T)) (llmk_residual_add).
+ *   _swiglu: w_gate_up [2 inter, in] (gate rows, then up rows); act[T, inter] =
+ *     llmk_swiglu(g, u) of g, u = fp16(norm(x) W^T) of the two halves.
+ *   _qkv_rope_scatter: w_qkv [(n_heads + 2 n_kv_heads) 64, in] (q, k, v rows, head_dim 64);
+ *     the projection's q, k and v rows go through llmk_qkv_rope_scatter with page size 16. */
+LLMK_API int llmk_linear_rows_norm(const uint16_t* x, const uint16_t* norm_w, float eps,
+                                   const uint16_t* w, uint16_t* y, int T, int in_features,
+                                   int out_features, void* stream);
+LLMK_API int llmk_linear_rows_residual(const uint16_t* x, const uint16_t* w, uint16_t* residual,
+                                       int T, int in_features, int out_features, void* stream);
+LLMK_API int llmk_linear_rows_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps,
+                                     const uint16_t* w_gate_up, uint16_t* act, int T,
+                                     int in_features, int inter, void* stream);
+LLMK_API int llmk_linear_rows_qkv_rope_scatter(const uint16_t* x, const uint16_t* norm_w,
+                                               float eps, const uint16_t* w_qkv,
+                                               uint16_t* q_out, uint16_t* k_pool,
+                                               uint16_t* v_pool, const int32_t* block_tables,
+                                               const int32_t* positions, const float* inv_freq,
+                                               int T, int in_features, int n_heads,
+                                               int n_kv_heads, int max_pages, void* stream);
+
 /* Chooses the algorithm of one shape by timing hipBLASLt's heuristic candidates with cold
  * caches, on `stream` with these operands (y is overwritten; synchronous; not while the stream
  * is capturing). Later llmk_linear calls of the shape use it. New entry point. */
@@ -339,6 +372,13 @@ LLMK_API void* llmk_engine_buffer(llmk_engine* e, int which, int layer);
 
 /* Refills every pool slot with 0x7F7F (fp16 NaN), as at creation. Not capturable. */
 LLMK_API int llmk_engine_reset_pools(llmk_engine* e, void* stream);
+
+/* Engine options (llmk_engine_set_option). LLMK_ENGINE_FUSE_FEW_ROWS (default 1): passes of at
+ * most LLMK_LINEAR_ROWS_MAX rows run the fused few-rows projections (llmk_linear_rows_*), which
+ * give the bits of the unfused pass in 6 launches per layer instead of 10; 0 runs the unfused
+ * pass. Changing it drops the cached graphs. New entry point. */
+#define LLMK_ENGINE_FUSE_FEW_ROWS 1
+LLMK_API int llmk_engine_set_option(llmk_engine* e, int option, int value);
 
 /* Tunes the GEMM plans of a forward pass over n_rows rows with n_logit_rows logit rows (< 0:
  * all rows) -- llmk_blas_tune on every projection shape. Overwrites the activation buffers (not

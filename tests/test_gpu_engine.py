@@ -110,6 +110,95 @@ def test_linear_rows_preconditions(llmk, blas):
     assert np.allclose(host(yy).view(np.float16).astype(np.float32), ref, atol=2e-2, rtol=2e-2)
 
 
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_linear_rows_fused_give_the_bits_of_the_separate_launches(llmk, orc, T):
+    """Each fused few-rows entry point against its unfused composition on the GPU (RMSNorm, the
+    few-rows projection, then residual_add / swiglu_rows / qkv_rope_scatter): every output bit,
+    pool slots included."""
+    rng = np.random.default_rng(0x5EED0230 + T)
+    H, eps = 2048, 1e-5
+    x = dev(normal_f16(rng, (T, H)))
+    nw = dev(normal_f16(rng, (H,), 1.0, 0.1))
+    normed = torch.empty(T * H, dtype=torch.float16, device=DEV)
+    llmk.rmsnorm(x, nw, normed, T, H, eps)
+
+    # norm prologue, plain store
+    N = 1000
+    w = dev(normal_f16(rng, (N, H), std=0.02))
+    y1 = torch.full((T * N,), float("nan"), dtype=torch.float16, device=DEV)
+    y2 = y1.clone()
+    llmk.linear_rows_norm(x, nw, eps, w, y1, T, H, N)
+    llmk.linear_rows(normed, w, y2, T, H, N)
+    y3 = y1.clone()
+    llmk.linear_rows_norm(x, None, eps, w, y3, T, H, N)
+    y4 = y1.clone()
+    llmk.linear_rows(x, w, y4, T, H, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(y1), host(y2)) and np.array_equal(host(y3), host(y4))
+
+    # residual-add epilogue (in = 8192, 16 waves per block for T <= 4)
+    K = 8192
+    a = dev(normal_f16(rng, (T, K)))
+    wd = dev(normal_f16(rng, (H, K), std=0.02))
+    r1 = dev(normal_f16(rng, (T, H)))
+    r2 = r1.clone()
+    llmk.linear_rows_residual(a, wd, r1, T, K, H)
+    p = torch.empty(T * H, dtype=torch.float16, device=DEV)
+    llmk.linear_rows(a, wd, p, T, K, H)
+    llmk.residual_add(r2, p, r2, T * H)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(r1), host(r2))
+
+    # norm prologue + swiglu epilogue
+    inter = 520
+    wgu = dev(normal_f16(rng, (2 * inter, H), std=0.05))
+    act1 = torch.full((T * inter,), float("nan"), dtype=torch.float16, device=DEV)
+    llmk.linear_rows_swiglu(x, nw, eps, wgu, act1, T, H, inter)
+    gu = torch.empty(T * 2 * inter, dtype=torch.float16, device=DEV)
+    llmk.linear_rows(normed, wgu, gu, T, H, 2 * inter)
+    act2 = act1.clone()
+    llmk.swiglu_rows(gu, act2, T, inter)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(act1), host(act2))
+
+    # norm prologue + RoPE / KV scatter epilogue
+    nh, nkv, hd, ps, max_pages = 32, 8, 64, 16, 6
+    qkvdim, kvdim = (nh + 2 * nkv) * hd, nkv * hd
+    num_pages = T * max_pages
+    wqkv = dev(normal_f16(rng, (qkvdim, H), std=0.05))
+    pos = dev_i32(rng.integers(0, max_pages * ps, T))
+    tables = dev_i32(rng.permutation(num_pages).reshape(T, max_pages))
+    inv = torch.from_numpy(orc.compute_rope_inv_freq(hd, 500000.0, 32.0, 1.0, 4.0,
+                                                     8192.0)).to(DEV)
+    pools = [dev(np.full(num_pages * ps * kvdim, POISON, np.uint16)) for _ in range(4)]
+    q1 = torch.full((T * nh * hd,), float("nan"), dtype=torch.float16, device=DEV)
+    q2 = q1.clone()
+    llmk.linear_rows_qkv_rope_scatter(x, nw, eps, wqkv, q1, pools[0], pools[1], tables, pos, inv,
+                                      T, H, nh, nkv, max_pages)
+    qkv = torch.empty(T * qkvdim, dtype=torch.float16, device=DEV)
+    llmk.linear_rows(normed, wqkv, qkv, T, H, qkvdim)
+    llmk.qkv_rope_scatter(qkv, qkvdim, q2, pools[2], pools[3], tables, pos, inv, T, max_pages,
+                          ps, nh, nkv, hd)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q1), host(q2))
+    assert np.array_equal(host(pools[0]), host(pools[2]))
+    assert np.array_equal(host(pools[1]), host(pools[3]))
+    assert int((host(pools[0]) != POISON).sum()) == T * kvdim  # one row per token, no more
+
+
+def test_linear_rows_fused_preconditions(llmk):
+    z = torch.zeros(8 * 8192 + 64, dtype=torch.float16, device=DEV)
+    w = torch.zeros(64 * 8192, dtype=torch.float16, device=DEV)
+    with pytest.raises(llmk.LlmkError, match="shape outside"):
+        llmk.linear_rows_norm(z, z, 1e-5, w, z, 8, 8192, 64)   # the norm of 8 rows of 8192
+    with pytest.raises(llmk.LlmkError, match="shape outside"):
+        llmk.linear_rows_swiglu(z, None, 1e-5, w, z, 2, 512, 6)  # inter % 4 != 0
+    with pytest.raises(llmk.LlmkError, match="aligned"):
+        llmk.linear_rows_norm(z, z[1:], 1e-5, w, z, 2, 512, 64)  # norm weight misaligned
+    llmk.linear_rows_norm(z, z, 1e-5, w, z, 4, 8192, 64)          # 4 rows of 8192: supported
+    torch.cuda.synchronize()
+
+
 def test_linear_after_tuning_matches_oracle(llmk, orc, blas):
     """llmk_blas_tune swaps a shape's algorithm for the fastest timed candidate; the result
     keeps the same bar."""
@@ -294,6 +383,44 @@ def test_engine_matches_oracle_small_model(llmk, orc):
         check_logits(orc, *s.step(parts), f"step {i}")
     written = s.check_pools(llmk)
     assert written[0] == int(s.len.sum())  # one slot per row ever run
+
+
+WIDE = dict(TINY, hidden=512, n_heads=8, n_kv_heads=2, inter=1024, vocab=1000)
+
+
+@pytest.mark.parametrize("n", [1, 3, 8])
+def test_engine_fused_few_rows_pass_gives_the_bits_of_the_unfused_pass(llmk, orc, n):
+    """A decode step of n <= 8 rows runs the fused few-rows projections (norms, RoPE + scatter,
+    SwiGLU and residual adds inside the projections). It must reproduce the unfused pass bit for
+    bit: logits, greedy tokens, residual stream and every pool of every layer."""
+    w = tiny_weights(0x5EED0250, embed_std=0.5, cfg=WIDE)
+    num_pages, max_pages = 64, 8
+    e = make_engine(llmk, WIDE, w, 16, max_pages, num_pages)
+    rng = np.random.default_rng(0x5EED0251 + n)
+    tables = rng.permutation(num_pages).astype(np.int32)[:n * max_pages].reshape(n, max_pages)
+    pos = rng.integers(0, max_pages * 16, n).astype(np.int32)
+    tok = rng.integers(0, WIDE["vocab"], n).astype(np.int32)
+    kvdim = WIDE["n_kv_heads"] * WIDE["head_dim"]
+    fill = torch.randn(num_pages * 16 * kvdim, device=DEV).half()
+
+    def run(fuse):
+        e.set_option(llmk.ENGINE_FUSE_FEW_ROWS, fuse)
+        for l in range(WIDE["n_layers"]):
+            for which in (llmk.BUF_K_POOL, llmk.BUF_V_POOL):
+                e.write_pool(which, l, fill)
+        e.set_rows(tok, pos, tables)
+        e.forward(n)
+        torch.cuda.synchronize()
+        got = [e.logits(n), e.next_tokens(n), e.residual(n)]
+        got += [e.pool(wh, l) for l in range(WIDE["n_layers"])
+                for wh in (llmk.BUF_K_POOL, llmk.BUF_V_POOL)]
+        return [t.clone().view(torch.int16) if t.dtype == torch.float16 else t.clone()
+                for t in got]
+
+    fused, plain = run(1), run(0)
+    assert not torch.isnan(fused[0].view(torch.float16)).any()
+    for a, b in zip(fused, plain):
+        assert torch.equal(a, b)
 
 
 def test_engine_graph_replays_match_eager(llmk, orc):
