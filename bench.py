@@ -48,16 +48,18 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--kernels", choices=["all", "headline", "step", "sched"], default="all",
-                    help="all: every configuration; headline: config 2 only; step: config 2 and "
-                         "the engine's decode step")
+    ap.add_argument("--kernels", choices=["all", "headline", "step", "step8", "sched"],
+                    default="all",
+                    help="all: every configuration; headline: config 2 only; step / step8: "
+                         "config 2 and the engine's decode step of 256 / 8 sequences; sched: "
+                         "config 2 and the reference's scheduler workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
                     help="summarise rocprofv3 csv output of this bench instead of running it")
-    ap.add_argument("--summarize-step", metavar="TRACE_DIR",
-                    help="per-kernel time of one engine decode step from a rocprofv3 kernel trace "
-                         "of `bench.py --kernels step`")
+    ap.add_argument("--summarize-step", nargs="+", metavar="TRACE_DIR [ROWS]",
+                    help="per-kernel time of one engine decode step of ROWS (256) sequences from "
+                         "a rocprofv3 kernel trace of `bench.py --kernels step` (or step8, 8)")
     return ap.parse_args()
 
 
@@ -182,10 +184,10 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
               f"traffic_bytes={traffic:.0f} algorithmic_bytes={alg} ratio={traffic / alg:.4f}")
 
 
-def summarize_step(trace_dir):
+def summarize_step(trace_dir, n_rows=256):
     """Kernels of the engine's decode step (the dispatches between the first and the last
-    embedding gather of 256 rows, i.e. the graph replays), grouped by kernel name and grid size:
-    launches per step, mean duration, and time per step."""
+    embedding gather of n_rows rows, i.e. the graph replays), grouped by kernel name and grid
+    size: launches per step, mean duration, and time per step."""
     import csv
     import glob
     rows = []
@@ -197,7 +199,7 @@ def summarize_step(trace_dir):
         return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
 
     starts = [i for i, r in enumerate(rows) if "k_embedding" in r["Kernel_Name"]
-              and grid(r) == 256 * 64]
+              and grid(r) == n_rows * 64]
     if len(starts) < 3:
         print("no decode steps found")
         return
@@ -210,7 +212,7 @@ def summarize_step(trace_dir):
     for r in steps:
         key = (r["Kernel_Name"], grid(r))
         agg.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    print(f"# engine decode step (Llama-3.2-1B shape, 256 rows), {n_steps} graph replays")
+    print(f"# engine decode step (Llama-3.2-1B shape, {n_rows} rows), {n_steps} graph replays")
     print("# launches/step  mean_us  us/step  grid  kernel")
     total = 0.0
     for (name, g), d in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
@@ -320,7 +322,8 @@ def main() -> int:
         summarize_profiles(*args.summarize_profiles)
         return 0
     if args.summarize_step:
-        summarize_step(args.summarize_step)
+        summarize_step(args.summarize_step[0],
+                       int(args.summarize_step[1]) if len(args.summarize_step) > 1 else 256)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the kernels are single-GPU; this build has no "
@@ -367,6 +370,8 @@ def main() -> int:
 
     if args.kernels == "step":
         kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W))
+    if args.kernels == "step8":
+        kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W, n_seqs=8))
     if args.kernels == "sched":
         kernels.update(bench_scheduler(llmk, wl, torch, np, dev))
 
@@ -497,6 +502,9 @@ def main() -> int:
         # new token each, every layer's K/V pool pre-filled for the cached positions; one HIP
         # graph per step (ref: engine/batched.cu:81-120, model_decode_batch_greedy :146-150)
         kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W))
+        # the same with 8 sequences: the fused few-rows pass (projections streaming the weights
+        # with the norms, RoPE + scatter, SwiGLU and residual adds inside them)
+        kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W, n_seqs=8))
 
         # continuous batching on the engine: the reference's scheduler workload, one request
         # at a time and up to 8 at once (ref: tests/test_scheduler.cu, engine/scheduler.cu)
@@ -535,11 +543,11 @@ def main() -> int:
     return 0
 
 
-def bench_decode_step(llmk, wl, timer, torch, np, dev, K, W) -> dict:
+def bench_decode_step(llmk, wl, timer, torch, np, dev, K, W, n_seqs=256) -> dict:
     import importlib
     weights = importlib.import_module("llmk.weights")
     cfg = llmk.ModelConfig()
-    lens = wl.attention_lens()
+    lens = wl.attention_lens(n_seqs)
     tokens, pos, tables, used = wl.decode_step_rows(lens)
     n = lens.size
     eng = llmk.Engine(cfg, max_rows=n, max_pages=128, num_pages=used)
@@ -571,17 +579,20 @@ def bench_decode_step(llmk, wl, timer, torch, np, dev, K, W) -> dict:
     steps = max(20, K // 4)
     t = timer.run(lambda i: graph.replay(), 1, steps, max(5, W // 4))
     nbytes = wl.bytes_decode_step(lens)
-    e = kernel_entry("decode step 1B, 256 seqs (graph)", nbytes, t, None, {
+    path = ("fused few-rows projections (libllmk) with the norms, RoPE + scatter, SwiGLU and "
+            "residual adds inside them" if n <= llmk.LINEAR_ROWS_MAX else
+            "hipBLASLt projections + libllmk kernels")
+    e = kernel_entry(f"decode step 1B, {n} seqs (graph)", nbytes, t, None, {
         "tokens_per_s": round(n / t["mean_s"], 1), "seqs": int(n),
         "context_tokens": int(lens.sum()), "layers": cfg.n_layers,
-        "note": "engine forward pass: hipBLASLt projections + libllmk kernels, one HIP graph; "
-                "bytes = sum of the step's kernels' algorithmic bytes (weights 2.47 GB, KV "
-                "cache reads, activations between kernels)"})
+        "note": f"engine forward pass: {path}, one HIP graph; bytes = sum of the step's "
+                "kernels' algorithmic bytes (weights 2.47 GB, KV cache reads, activations "
+                "between kernels)"})
     log(f"    -> {e['tokens_per_s']:.0f} tokens/s")
     eng.close()
     del graph
     torch.cuda.empty_cache()
-    return {"decode_step_1b_256": e}
+    return {f"decode_step_1b_{n}": e}
 
 
 def bench_scheduler(llmk, wl, torch, np, dev) -> dict:

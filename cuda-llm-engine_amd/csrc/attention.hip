@@ -226,7 +226,10 @@ struct MergeLds {
 // the block's combined unnormalised state of query head kvg * HEADS + t / 8, dims 8 * (t % 8)
 // .. + 8: A (sum of p * v), M (max score, log2 units) and L (sum of p). Ends with a barrier, so
 // the LDS can be reused at once.
-template <int KVW>
+// NJ > 0: the wave has at most NJ chunks whose every position is cached; their loads are all
+// issued before the first fold (one round trip for a short segment). NJ = 0: any number, streamed
+// two at a time.
+template <int KVW, int NJ = 0>
 __device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
                                                const f16* __restrict__ k_pool,
                                                const f16* __restrict__ v_pool,
@@ -274,7 +277,20 @@ __device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
   bool all[ROWS];  // unused by the FULL fold
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) all[i] = true;
-  if (nj > 0) {
+  if constexpr (NJ > 0) {
+    if (nj > 0) {
+      // Slots past the wave's last chunk load that chunk again (in bounds, and unconditional, so
+      // that each fold waits only for its own loads); they are not folded.
+      Chunk<KVW> c[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        load_chunk<KVW>(c[j], k_pool, v_pool, table, pos0, first + (j < nj ? j : nj - 1) * STEP,
+                        row_halves, lane_off, row_step);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (j < nj) fold_chunk<KVW, true>(st, qv, c[j], all);
+    }
+  } else if (nj > 0) {
     Chunk<KVW> a, b;
     load_chunk<KVW>(a, k_pool, v_pool, table, pos0, first, row_halves, lane_off,
                     row_step);
@@ -359,8 +375,9 @@ __device__ __forceinline__ void store_nan(f16* __restrict__ out, int seq, int h,
 }
 
 // Sequence-split grid (num_splits, kv groups, n_seq): block (split, g, s) takes pages
-// [split * pages_per_split, +pages_per_split) of sequence s. Used with one or two splits.
-template <int KVW>
+// [split * pages_per_split, +pages_per_split) of sequence s. Used with one or two splits, and for
+// small batches cut into runs of at most 4 pages (NJ: as in attend_segment).
+template <int KVW, int NJ>
 __global__ void __launch_bounds__(kThreads)
 k_attn_split(const f16* __restrict__ q, const f16* __restrict__ k_pool,
              const f16* __restrict__ v_pool, const int* __restrict__ block_tables,
@@ -382,8 +399,8 @@ k_attn_split(const f16* __restrict__ q, const f16* __restrict__ k_pool,
   const int page1 = page0 + pages_per_split < P ? page0 + pages_per_split : P;
   const int pos1 = S < page1 * kPage ? S : page1 * kPage;
   float A[8], M, L;
-  attend_segment<KVW>(q, k_pool, v_pool, block_tables + (size_t)seq * max_pages, seq,
-                      page0 * kPage, pos1, kvg, n_heads, n_kv_heads, lds, A, M, L);
+  attend_segment<KVW, NJ>(q, k_pool, v_pool, block_tables + (size_t)seq * max_pages, seq,
+                          page0 * kPage, pos1, kvg, n_heads, n_kv_heads, lds, A, M, L);
   if (!writer) return;
   if ((P + pages_per_split - 1) / pages_per_split == 1)
     store_out(out, seq, h, n_heads, A, L);
@@ -540,91 +557,100 @@ k_attn_balanced(const f16* __restrict__ q, const f16* __restrict__ k_pool,
   }
 }
 
-// Grid (ceil(n_heads / 32), n_seq), 256 threads: thread (head, 8 dims). Merges the splits of
-// every sequence that has more than one. pages_per_split > 0: the sequence-split grid's
-// layout, splits = ceil(P / pages_per_split), empty sequences already written. 0: the
-// page-balanced layout, the segment count read from the sequence's last slot. The partials are
-// folded in four at a time, their loads issued together, with a running maximum.
+// Grid (ceil(n_heads / 4), n_seq), 256 threads: wave w merges the pieces of query head
+// 4 * blockIdx.x + w of sequence blockIdx.y, for every sequence that has more than one.
+// pages_per_split > 0: the sequence-split grid's layout, pieces = ceil(P / pages_per_split),
+// empty sequences already written. 0: the page-balanced layout, the piece count read from the
+// sequence's last slot. Lane (sg = lane / 16, dq = lane % 16) folds pieces sg, sg + 4, ... for
+// dims 4 dq .. 4 dq + 3; all of a round's loads (32 pieces per wave) are issued together, so a
+// sequence of up to 32 pieces costs one round trip. The four piece groups then meet in two
+// exchanges across rows. The running maximum M is shared by the whole wave, so every lane's
+// partial sums carry the same scale.
+constexpr int kMergePer = 8;  // pieces per lane per round
+
+__device__ __forceinline__ void store_nan4(f16* __restrict__ out, int seq, int h, int n_heads,
+                                           int dq) {
+  const uint32_t nan = 0x7E007E00u;
+  *reinterpret_cast<uint2*>(out + ((size_t)seq * n_heads + h) * kHeadDim + 4 * dq) =
+      make_uint2(nan, nan);
+}
+
 __global__ void __launch_bounds__(256)
 k_attn_merge(const float* __restrict__ part_o, const float2* __restrict__ part_ml,
              const int* __restrict__ seq_lens, f16* __restrict__ out, int max_pages, int n_heads,
              int num_splits, int pages_per_split) {
-  constexpr int kBatch = 4;
   const int seq = blockIdx.y;
-  const int h = blockIdx.x * 32 + (threadIdx.x >> 3), e8 = threadIdx.x & 7;
+  const int h = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (h >= n_heads) return;
-  const size_t base = (size_t)seq * num_splits * n_heads + h;  // slot of split 0
-  // The first batch of slots is loaded together with the length and the segment count; slots
-  // beyond the count hold stale data and are masked below (they lie inside the workspace).
-  float2 ml[kBatch];
-  u32x4 a0[kBatch], a1[kBatch];
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int j = 0; j < kBatch; ++j) {
-    const size_t k = base + (size_t)j * n_heads;
-    const bool in = j < num_splits;
-    ml[j] = in ? part_ml[k] : make_float2(-INFINITY, 0.0f);
-    a0[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8) : zero;
-    a1[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8 + 4) : zero;
-  }
+  const int lane = threadIdx.x & 63, sg = lane >> 4, dq = lane & 15;
+  const size_t base = (size_t)seq * num_splits * n_heads + h;  // slot of piece 0
   const int S = seq_lens[seq];
-  const float2 meta =
-      pages_per_split > 0 ? make_float2(0.0f, 0.0f)
-                          : part_ml[((size_t)seq * num_splits + num_splits - 1) * n_heads];
   const int P = seq_pages(S, max_pages);
   int used;
   if (pages_per_split > 0) {
     used = (P + pages_per_split - 1) / pages_per_split;
   } else {
     if (P == 0) {
-      store_nan(out, seq, h, n_heads);
+      if (sg == 0) store_nan4(out, seq, h, n_heads, dq);
       return;
     }
-    used = __builtin_bit_cast(int, meta.x);
+    used = __builtin_bit_cast(
+        int, part_ml[((size_t)seq * num_splits + num_splits - 1) * n_heads].x);
   }
   if (used <= 1) return;
-  float M = -INFINITY, L = 0.0f, A[8];
+  float M = -INFINITY, L = 0.0f, A[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < used; s0 += 4 * kMergePer) {
+    float2 ml[kMergePer];
+    float4 a[kMergePer];
 #pragma unroll
-  for (int d = 0; d < 8; ++d) A[d] = 0.0f;
-  for (int s0 = 0; s0 < used; s0 += kBatch) {
-    if (s0 > 0) {
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const size_t k = base + (size_t)(s0 + j) * n_heads;
-        const bool in = s0 + j < used;
-        ml[j] = in ? part_ml[k] : make_float2(-INFINITY, 0.0f);
-        a0[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8) : zero;
-        a1[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8 + 4) : zero;
+    for (int j = 0; j < kMergePer; ++j) {
+      const int piece = s0 + sg + 4 * j;
+      const size_t k = base + (size_t)piece * n_heads;
+      ml[j] = make_float2(-INFINITY, 0.0f);  // no piece: weight exp2(-inf) = 0
+      a[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (piece < used) {
+        ml[j] = part_ml[k];
+        a[j] = *reinterpret_cast<const float4*>(part_o + k * kHeadDim + 4 * dq);
       }
     }
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j)
-      if (s0 + j >= used) {  // stale slot (may hold NaN): weight 0 and zero data
-        ml[j] = make_float2(-INFINITY, 0.0f);
-        a0[j] = zero;
-        a1[j] = zero;
-      }
     float mx = M;
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) mx = fmaxf(mx, ml[j].x);
-    const float corr = __builtin_amdgcn_exp2f(M - mx);  // first batch: M = -inf -> 0
+    for (int j = 0; j < kMergePer; ++j) mx = fmaxf(mx, ml[j].x);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float corr = __builtin_amdgcn_exp2f(M - mx);  // first round: M = -inf -> 0
     L = L * corr;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) A[d] = A[d] * corr;
+    for (int d = 0; d < 4; ++d) A[d] = A[d] * corr;
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const float w = __builtin_amdgcn_exp2f(ml[j].x - mx);  // masked slot: exp2(-inf) = 0
+    for (int j = 0; j < kMergePer; ++j) {
+      const float w = __builtin_amdgcn_exp2f(ml[j].x - mx);
       L = __builtin_fmaf(ml[j].y, w, L);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t x0 = elem(a0[j], d), x1 = elem(a1[j], d);
-        A[d] = __builtin_fmaf(__builtin_bit_cast(float, x0), w, A[d]);
-        A[d + 4] = __builtin_fmaf(__builtin_bit_cast(float, x1), w, A[d + 4]);
-      }
+      A[0] = __builtin_fmaf(a[j].x, w, A[0]);
+      A[1] = __builtin_fmaf(a[j].y, w, A[1]);
+      A[2] = __builtin_fmaf(a[j].z, w, A[2]);
+      A[3] = __builtin_fmaf(a[j].w, w, A[3]);
     }
     M = mx;
   }
-  store_out(out, seq, h, n_heads, A, L);
+  L = L + __shfl_xor(L, 16);
+  L = L + __shfl_xor(L, 32);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    A[d] = A[d] + __shfl_xor(A[d], 16);
+    A[d] = A[d] + __shfl_xor(A[d], 32);
+  }
+  if (sg == 0) {
+    f16 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] = (f16)(A[d] / L);
+    uint2 v;
+    v.x = (uint32_t)__builtin_bit_cast(uint16_t, o[0]) |
+          ((uint32_t)__builtin_bit_cast(uint16_t, o[1]) << 16);
+    v.y = (uint32_t)__builtin_bit_cast(uint16_t, o[2]) |
+          ((uint32_t)__builtin_bit_cast(uint16_t, o[3]) << 16);
+    *reinterpret_cast<uint2*>(out + ((size_t)seq * n_heads + h) * kHeadDim + 4 * dq) = v;
+  }
 }
 
 // Blocks of k_attn_balanced<KVW> that fit on the device at once (cached per device).
@@ -655,27 +681,61 @@ struct AttnArgs {
   int n_seq, max_pages, n_heads, n_kv_heads, num_splits;
 };
 
+// Batches of at most this many (sequence, kv group) pairs whose splits are at most
+// kShortRunPages pages long take the sequence-split grid: there is no length scan, and a block's
+// few chunks are in flight together. Larger batches, or longer runs, take the page-balanced
+// grid, which follows the actual lengths. Measured at 8 sequences of lengths uniform in
+// [1, 2048], both kernels together: 12.1 us with 4-page runs against 16.1 us page-balanced.
+constexpr int kSplitGridPairs = 16;
+constexpr int kShortRunPages = 4;
+
+// attend_segment's NJ for runs of pps pages: all of a wave's chunks in flight at once when it
+// has at most two (4 chunks cost 188 VGPRs, and the lost occupancy outweighed the gain), else 0.
+template <int KVW>
+int short_run_chunks(int pps) {
+  constexpr int PPL = 8 / KVW, ROWS = chunk_rows<KVW>();
+  const int rows = pps * kPage / PPL;
+  const int per_wave = ((rows + ROWS - 1) / ROWS + kWaves - 1) / kWaves;
+  return per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : 0;
+}
+
+template <int KVW, int NJ>
+int split_launch(const AttnArgs& a, int groups, int pps, hipStream_t s) {
+  const dim3 grid((unsigned)a.num_splits, (unsigned)groups, (unsigned)a.n_seq);
+  return launch(k_attn_split<KVW, NJ>, grid, dim3(kThreads), 0, s, a.q, a.k_pool, a.v_pool,
+                a.tables, a.lens, a.out, a.part_o, a.part_ml, a.max_pages, a.n_heads,
+                a.n_kv_heads, a.num_splits, pps);
+}
+
 template <int KVW>
 int attn_launch(const AttnArgs& a, hipStream_t s) {
   const int groups = a.n_kv_heads >= 8 ? a.n_kv_heads / 8 : 1;
-  if (a.num_splits >= 3 && a.part_o) {
+  const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;  // pages per split
+  const bool short_runs = a.part_o && a.num_splits >= 3 && pps <= kShortRunPages &&
+                          (long long)a.n_seq * groups <= kSplitGridPairs;
+  if (a.num_splits >= 3 && a.part_o && !short_runs) {
     int blocks = resident_blocks<KVW>() / groups;
     if (blocks < 1) blocks = 1;
     int st = launch(k_attn_balanced<KVW>, dim3((unsigned)blocks, (unsigned)groups), dim3(kThreads),
                     0, s, a.q, a.k_pool, a.v_pool, a.tables, a.lens, a.out, a.part_o, a.part_ml,
                     a.n_seq, a.max_pages, a.n_heads, a.n_kv_heads, a.num_splits);
     if (st != 0) return st;
-    const dim3 mgrid((unsigned)((a.n_heads + 31) / 32), (unsigned)a.n_seq);
+    const dim3 mgrid((unsigned)((a.n_heads + 3) / 4), (unsigned)a.n_seq);
     return launch(k_attn_merge, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,
                   a.max_pages, a.n_heads, a.num_splits, 0);
   }
-  const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;  // pages per split
-  const dim3 grid((unsigned)a.num_splits, (unsigned)groups, (unsigned)a.n_seq);
-  int st = launch(k_attn_split<KVW>, grid, dim3(kThreads), 0, s, a.q, a.k_pool, a.v_pool,
-                  a.tables, a.lens, a.out, a.part_o, a.part_ml, a.max_pages, a.n_heads,
-                  a.n_kv_heads, a.num_splits, pps);
+  int st;
+  if (short_runs) {
+    switch (short_run_chunks<KVW>(pps)) {
+      case 1: st = split_launch<KVW, 1>(a, groups, pps, s); break;
+      case 2: st = split_launch<KVW, 2>(a, groups, pps, s); break;
+      default: st = split_launch<KVW, 0>(a, groups, pps, s); break;
+    }
+  } else {
+    st = split_launch<KVW, 0>(a, groups, pps, s);
+  }
   if (st != 0 || pps >= a.max_pages) return st;  // every sequence fits in one split
-  const dim3 mgrid((unsigned)((a.n_heads + 31) / 32), (unsigned)a.n_seq);
+  const dim3 mgrid((unsigned)((a.n_heads + 3) / 4), (unsigned)a.n_seq);
   return launch(k_attn_merge, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,
                 a.max_pages, a.n_heads, a.num_splits, pps);
 }

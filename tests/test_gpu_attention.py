@@ -95,6 +95,29 @@ def test_other_kv_head_counts(llmk, orc, nkv):
         assert_tol(cmp, 0.75, f"n_kv {nkv} splits {splits}")
 
 
+@pytest.mark.parametrize("splits", [32, 43, 64, 128])
+def test_small_batch_in_short_runs(llmk, orc, reference_case, splits):
+    """A small batch cut into runs of at most 4 pages takes the sequence-split grid: 4, 3, 2 and
+    1 pages per split of a 128-page table (the last one folds 128 pieces of the 2048-position
+    sequence, four rounds of the merge)."""
+    d = OnDevice(reference_case)
+    cmp = orc.compare(d.run(llmk, splits), oracle_out(orc, reference_case))
+    assert_tol(cmp, 0.75, f"short runs, splits {splits}")
+
+
+@pytest.mark.parametrize("nkv", [1, 2, 4, 16])
+def test_short_runs_with_other_kv_head_counts(llmk, orc, nkv):
+    """Short runs with rows of 1, 2 or 4 kv heads (several positions per row read) and with 16
+    kv heads (two kv groups): 32-page tables cut into runs of 1, 2 and 4 pages."""
+    c = attention_case(np.random.default_rng(100 + nkv), (1, 7, 16, 33, 130, 500),
+                       n_heads=4 * nkv, n_kv_heads=nkv)
+    assert c["max_pages"] == 32
+    d = OnDevice(c)
+    ref = oracle_out(orc, c)
+    for splits in (8, 16, 32):
+        assert_tol(orc.compare(d.run(llmk, splits), ref), 0.75, f"n_kv {nkv} splits {splits}")
+
+
 def test_empty_sequences_give_nan_and_leave_the_rest_intact(llmk, orc):
     c = attention_case(np.random.default_rng(5), (0, 5, -3, 40))
     d = OnDevice(c)
