@@ -430,7 +430,7 @@ static bool fused_rows_path(const llmk_engine* e, int n) {
   if (!e->fuse_rows || n > LLMK_LINEAR_ROWS_MAX) return false;
   const int steps = m.hidden / 512;  // the norm prologue: one 512-wide step per wave
   return m.hidden % 512 == 0 && e->qdim % 512 == 0 && m.inter % 512 == 0 && m.head_dim == 64 &&
-         (steps & (steps - 1)) == 0 && steps <= (n > 4 ? 8 : 16);
+         (steps & (steps - 1)) == 0 && steps <= 16;
 }
 
 static int forward_fused_rows(llmk_engine* e, int n, int nl, bool all_rows, int num_splits,

@@ -16,7 +16,12 @@
 //   - The 8 * TP partial sums of a lane are then reduced over the wave in a halving butterfly:
 //     at each exchange a lane keeps half of its values and adds its partner's copy of them, so
 //     the 64 lanes end up holding distinct (row, token) sums after 63 adds (mostly DPP) instead
-//     of 8 * TP full reductions. The waves' sums meet in LDS.
+//     of 8 * TP full reductions. The value index is token-major (t * 8 + r), so the exchanges
+//     that pair tokens come first and run row by row, right after the row's dot products: a
+//     lane holds the TP sums of one row and 8 per-row shares, not 8 * TP sums (at T = 8: 91
+//     VGPRs, 5 waves per SIMD, against 130 and 3). The waves' sums meet in LDS.
+//   - A normalising launch stages each wave's raw x slice in LDS once; the norms are taken from
+//     there instead of every wave re-reading whole rows.
 // Summation order differs from cuBLAS/hipBLASLt (lane-strided partial sums, then the butterfly),
 // so results agree with the fp32 dot product to fp32 rounding, not bit for bit.
 #include "common.hpp"
@@ -61,8 +66,8 @@ __device__ __forceinline__ float partner(float v) {
   else return __shfl_xor(v, kMask[S]);
 }
 
-template <int N, int S>
-__device__ __forceinline__ void butterfly(float (&v)[64]) {
+template <int N, int S, int M>
+__device__ __forceinline__ void butterfly(float (&v)[M]) {
   if constexpr (S < 6) {
     if constexpr (N > 1) {
       const bool up = (threadIdx.x & kMask[S]) != 0;
@@ -79,6 +84,25 @@ __device__ __forceinline__ void butterfly(float (&v)[64]) {
     }
   }
 }
+
+// The halving exchanges S, S + 1, ... of the butterfly on v[0 .. N) until one value is left
+// (no full adds): v[0] then holds the lane's share.
+template <int N, int S, int M>
+__device__ __forceinline__ void halve(float (&v)[M]) {
+  if constexpr (N > 1) {
+    const bool up = (threadIdx.x & kMask[S]) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      const float send = up ? v[i] : v[i + N / 2];
+      const float keep = up ? v[i + N / 2] : v[i];
+      v[i] = keep + partner<S>(send);
+    }
+    halve<N / 2, S + 1>(v);
+  }
+}
+
+template <int N>
+constexpr int log2c() { return N <= 1 ? 0 : 1 + log2c<N / 2>(); }
 
 // After butterfly<N, 0>: the value index whose total lane `lane` holds (its bits, from the top,
 // are the lane's bits kMask[0], kMask[1], ... of the halving exchanges), and whether the lane is
@@ -159,9 +183,23 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
   const int in = a.in, T = a.T;
   const int steps = in / kStep;
 
-  float v[64];
+  // Token-major value index t * 8 + r: the butterfly's first log2(TP) halvings pair tokens of
+  // one row, so they run row by row right after its dot products, and only the row's TP sums
+  // and the 8 per-row shares are live.
+  constexpr int LT = log2c<TP>();
+  float red[kRows];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) v[i] = 0.0f;
+  for (int r = 0; r < kRows; ++r) red[r] = 0.0f;
+  auto rows_dot = [&](const u32x4 (&wv)[kRows], const u32x4 (&xv)[TP]) {
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      float acc[TP];
+#pragma unroll
+      for (int t = 0; t < TP; ++t) acc[t] = dot8(wv[r], xv[t], 0.0f);
+      halve<TP, 0>(acc);
+      red[r] = red[r] + acc[0];
+    }
+  };
   const f16* wr[kRows];
 #pragma unroll
   for (int r = 0; r < kRows; ++r) wr[r] = a.w + (size_t)row_of<EPI>(b, r, a) * in + lane * 8;
@@ -170,40 +208,39 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
   for (int t = 0; t < TP; ++t) xr[t] = a.x + (size_t)(t < T ? t : T - 1) * in + lane * 8;
 
   if constexpr (NORM) {
-    // The rows whose norms this wave takes (t = wave + WV q), loaded first so that waiting for
-    // them does not wait for the W loads issued after them.
-    constexpr int NQ = (TP + WV - 1) / WV;
-    u32x4 nr[NQ][WV];
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const int t = (wave + WV * q) % TP;  // waves past the last row repeat one (not stored)
-      const f16* row = a.x + (size_t)(t < T ? t : T - 1) * in + lane * 8;
-#pragma unroll
-      for (int k = 0; k < WV; ++k) nr[q][k] = ld16(row + (size_t)k * kStep);
-    }
+    // Every wave loads its step of all TP rows (x first: the norms wait only for those) and
+    // leaves the raw slices in LDS; wave t % WV then sums the squares of row t from there, in
+    // the RMSNorm kernel's order.
+    __shared__ u32x4 xs[TP][WV][64];
     const size_t k0 = (size_t)wave * kStep;  // this wave's one step
     u32x4 wv[kRows], xv[TP];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) wv[r] = ld16_stream(wr[r] + k0);
-#pragma unroll
     for (int t = 0; t < TP; ++t) xv[t] = ld16(xr[t] + k0);
     const u32x4 nw = ld16(a.norm_w + k0 + lane * 8);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) wv[r] = ld16_stream(wr[r] + k0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
+    for (int t = 0; t < TP; ++t) xs[t][wave][lane] = xv[t];
+    __syncthreads();
+    constexpr int NQ = (TP + WV - 1) / WV;
+#pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      float ss = 0.0f;
-#pragma unroll
-      for (int k = 0; k < WV; ++k) {
-        const f16x8 h = as_h8(nr[q][k]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float f = (float)h[j];
-          ss = ss + f * f;
-        }
-      }
-      ss = wave_sum(ss);
       const int t = wave + WV * q;
-      if (lane == 0 && t < TP) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
+      if (t < TP) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < WV; ++k) {
+          const f16x8 h = as_h8(xs[t][k][lane]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float f = (float)h[j];
+            ss = ss + f * f;
+          }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -215,10 +252,7 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
       for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
       xv[t] = as_u4(as_h8(nw) * an);
     }
-#pragma unroll
-    for (int r = 0; r < kRows; ++r)
-#pragma unroll
-      for (int t = 0; t < TP; ++t) v[r * TP + t] = dot8(wv[r], xv[t], v[r * TP + t]);
+    rows_dot(wv, xv);
   } else {
     for (int s = wave; s < steps; s += WV) {
       const size_t k = (size_t)s * kStep;
@@ -230,16 +264,15 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
       // Every load of the step is in flight before the first product (left alone, the
       // scheduler reuses one register for the W rows and waits for each load in turn).
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int r = 0; r < kRows; ++r)
-#pragma unroll
-        for (int t = 0; t < TP; ++t) v[r * TP + t] = dot8(wv[r], xv[t], v[r * TP + t]);
+      rows_dot(wv, xv);
     }
   }
 
-  butterfly<N, 0>(v);
+  butterfly<kRows, LT>(red);
   bool writer;
-  const int idx = butterfly_index<N>(lane, &writer);
+  const int tidx = butterfly_index<N>(lane, &writer);  // t * 8 + r
+  const int idx = (tidx % kRows) * TP + tidx / kRows;  // the epilogue's r * TP + t
+  const float* v = red;
   if (writer) part[wave][idx] = v[0];
   __syncthreads();
   auto total = [&](int i) {
@@ -290,12 +323,11 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
   }
 }
 
-// Waves per block: one per step of the in dimension, up to 16 (8 with 8 rows, whose 130
-// registers a 1024-thread block cannot give every wave). A normalising launch needs exactly one
-// step per wave, so steps must be 1, 2, 4, 8 or 16 (at most 8 with 8 rows); 0 otherwise.
+// Waves per block: one per step of the in dimension, up to 16. A normalising launch needs
+// exactly one step per wave, so steps must be 1, 2, 4, 8 or 16; 0 otherwise.
 template <int TP>
 int rows_waves(int steps, bool norm) {
-  const int cap = TP < 8 ? 16 : 8;
+  const int cap = 16;
   if (norm) {
     const bool pow2 = (steps & (steps - 1)) == 0;
     return steps >= 1 && steps <= cap && pow2 ? steps : 0;
@@ -312,8 +344,7 @@ int rows_launch_tp(const RowsArgs& a, unsigned blocks, hipStream_t s) {
     case 4: return launch(k_rows<TP, 4, EPI, NORM>, dim3(blocks), dim3(256), 0, s, a);
     case 8: return launch(k_rows<TP, 8, EPI, NORM>, dim3(blocks), dim3(512), 0, s, a);
     case 16:
-      if constexpr (TP < 8) return launch(k_rows<TP, 16, EPI, NORM>, dim3(blocks), dim3(1024), 0, s, a);
-      return LLMK_ERR_UNSUPPORTED;
+      return launch(k_rows<TP, 16, EPI, NORM>, dim3(blocks), dim3(1024), 0, s, a);
     default: return LLMK_ERR_UNSUPPORTED;
   }
 }
@@ -340,7 +371,7 @@ int rows_common(RowsArgs* a, const uint16_t* x, const uint16_t* norm_w, float ep
   if ((size_t)out > (size_t)0xFFFFFFFFu * kRows) return LLMK_ERR_UNSUPPORTED;
   if (norm_w) {
     const int steps = in / kStep;
-    const int wv = T > 4 ? rows_waves<8>(steps, true) : rows_waves<4>(steps, true);
+    const int wv = rows_waves<8>(steps, true);
     if (wv == 0) return LLMK_ERR_UNSUPPORTED;
     if (!aligned16(norm_w)) return LLMK_ERR_ALIGNMENT;
   }

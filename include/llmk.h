@@ -244,9 +244,8 @@ LLMK_API int llmk_linear_rows(const uint16_t* x, const uint16_t* w, uint16_t* y,
 /* The few-rows projection with the decode step's neighbouring element-wise work done in the same
  * kernel (T <= LLMK_LINEAR_ROWS_MAX, in_features % 512 == 0, 16-byte aligned operands). With
  * norm_w non-null the x rows are first RMSNorm-ed with weight norm_w [in_features] and eps,
- * giving the bits llmk_rmsnorm gives (in_features / 512 a power of two up to 16, or up to 8
- * with T > 4); with
- * norm_w null x is used as is. Each epilogue rounds the projection to fp16 first and then
+ * giving the bits llmk_rmsnorm gives (in_features / 512 a power of two up to 16); with norm_w
+ * null x is used as is. Each epilogue rounds the projection to fp16 first and then
  * applies the reference's formula, so every result has the bits of llmk_linear_rows followed
  * by the separate launch. New entry points, for the engine's decode steps with few sequences;
  * they replace ref: engine/batched.cu:51-58 (rmsnorm, three projections, rope_apply, two

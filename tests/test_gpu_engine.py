@@ -190,12 +190,12 @@ def test_linear_rows_fused_preconditions(llmk):
     z = torch.zeros(8 * 8192 + 64, dtype=torch.float16, device=DEV)
     w = torch.zeros(64 * 8192, dtype=torch.float16, device=DEV)
     with pytest.raises(llmk.LlmkError, match="shape outside"):
-        llmk.linear_rows_norm(z, z, 1e-5, w, z, 8, 8192, 64)   # the norm of 8 rows of 8192
+        llmk.linear_rows_norm(z, z, 1e-5, w, z, 2, 16384, 32)  # the norm of rows of 16384
     with pytest.raises(llmk.LlmkError, match="shape outside"):
         llmk.linear_rows_swiglu(z, None, 1e-5, w, z, 2, 512, 6)  # inter % 4 != 0
     with pytest.raises(llmk.LlmkError, match="aligned"):
         llmk.linear_rows_norm(z, z[1:], 1e-5, w, z, 2, 512, 64)  # norm weight misaligned
-    llmk.linear_rows_norm(z, z, 1e-5, w, z, 4, 8192, 64)          # 4 rows of 8192: supported
+    llmk.linear_rows_norm(z, z, 1e-5, w, z, 8, 8192, 64)          # 8 rows of 8192: supported
     torch.cuda.synchronize()
 
 
