@@ -425,6 +425,9 @@ extern "C" int llmk_engine_set_rows(llmk_engine* e, int n_rows, const int32_t* t
 // Whether a pass over n rows takes the fused few-rows path: every projection is a
 // llmk_linear_rows_* call with the norms, RoPE + scatter, SwiGLU and residual adds in its
 // prologue or epilogue (5 + 1 launches per layer instead of 9 + 1).
+// Logit rows from which the fused pass normalises the lm head's input in a launch of its own.
+constexpr int kLmSeparateNormRows = 4;
+
 static bool fused_rows_path(const llmk_engine* e, int n) {
   const llmk_model_config& m = e->cfg;
   if (!e->fuse_rows || n > LLMK_LINEAR_ROWS_MAX) return false;
@@ -461,8 +464,15 @@ static int forward_fused_rows(llmk_engine* e, int n, int nl, bool all_rows, int 
     LLMK_TRY(llmk_embedding_lookup(e->x, e->logit_rows, e->fin, nl, H, s));
     lm_in = e->fin;
   }
-  LLMK_TRY(llmk_linear_rows_norm(lm_in, e->final_norm, m.eps, e->embed, e->logits, nl, H,
-                                 m.vocab, s));
+  if (nl >= kLmSeparateNormRows) {
+    // Each of the lm head's vocab / 8 blocks would normalise all of its rows again; a separate
+    // RMSNorm launch costs less from a few rows up (the same bits either way).
+    LLMK_TRY(llmk_rmsnorm(lm_in, e->final_norm, e->normed, nl, H, m.eps, s));
+    LLMK_TRY(llmk_linear_rows(e->normed, e->embed, e->logits, nl, H, m.vocab, s));
+  } else {
+    LLMK_TRY(llmk_linear_rows_norm(lm_in, e->final_norm, m.eps, e->embed, e->logits, nl, H,
+                                   m.vocab, s));
+  }
   LLMK_TRY(llmk_argmax_rows(e->logits, e->next, nl, m.vocab, s));
 #undef LLMK_TRY
   return LLMK_OK;
