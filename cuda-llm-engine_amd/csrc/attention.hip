@@ -557,15 +557,107 @@ k_attn_balanced(const f16* __restrict__ q, const f16* __restrict__ k_pool,
   }
 }
 
-// Grid (ceil(n_heads / 4), n_seq), 256 threads: wave w merges the pieces of query head
+// Merge for a few pieces per sequence (the page-balanced grid, one or two splits). Grid
+// (ceil(n_heads / 32), n_seq), 256 threads: thread (head, 8 dims). Merges the pieces of every
+// sequence that has more than one. pages_per_split > 0: the sequence-split grid's
+// layout, splits = ceil(P / pages_per_split), empty sequences already written. 0: the
+// page-balanced layout, the segment count read from the sequence's last slot. The partials are
+// folded in four at a time, their loads issued together, with a running maximum.
+__global__ void __launch_bounds__(256)
+k_attn_merge(const float* __restrict__ part_o, const float2* __restrict__ part_ml,
+             const int* __restrict__ seq_lens, f16* __restrict__ out, int max_pages, int n_heads,
+             int num_splits, int pages_per_split) {
+  constexpr int kBatch = 4;
+  const int seq = blockIdx.y;
+  const int h = blockIdx.x * 32 + (threadIdx.x >> 3), e8 = threadIdx.x & 7;
+  if (h >= n_heads) return;
+  const size_t base = (size_t)seq * num_splits * n_heads + h;  // slot of split 0
+  // The first batch of slots is loaded together with the length and the segment count; slots
+  // beyond the count hold stale data and are masked below (they lie inside the workspace).
+  float2 ml[kBatch];
+  u32x4 a0[kBatch], a1[kBatch];
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j) {
+    const size_t k = base + (size_t)j * n_heads;
+    const bool in = j < num_splits;
+    ml[j] = in ? part_ml[k] : make_float2(-INFINITY, 0.0f);
+    a0[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8) : zero;
+    a1[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8 + 4) : zero;
+  }
+  const int S = seq_lens[seq];
+  const float2 meta =
+      pages_per_split > 0 ? make_float2(0.0f, 0.0f)
+                          : part_ml[((size_t)seq * num_splits + num_splits - 1) * n_heads];
+  const int P = seq_pages(S, max_pages);
+  int used;
+  if (pages_per_split > 0) {
+    used = (P + pages_per_split - 1) / pages_per_split;
+  } else {
+    if (P == 0) {
+      store_nan(out, seq, h, n_heads);
+      return;
+    }
+    used = __builtin_bit_cast(int, meta.x);
+  }
+  if (used <= 1) return;
+  float M = -INFINITY, L = 0.0f, A[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) A[d] = 0.0f;
+  for (int s0 = 0; s0 < used; s0 += kBatch) {
+    if (s0 > 0) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const size_t k = base + (size_t)(s0 + j) * n_heads;
+        const bool in = s0 + j < used;
+        ml[j] = in ? part_ml[k] : make_float2(-INFINITY, 0.0f);
+        a0[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8) : zero;
+        a1[j] = in ? ld16(part_o + k * kHeadDim + e8 * 8 + 4) : zero;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      if (s0 + j >= used) {  // stale slot (may hold NaN): weight 0 and zero data
+        ml[j] = make_float2(-INFINITY, 0.0f);
+        a0[j] = zero;
+        a1[j] = zero;
+      }
+    float mx = M;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) mx = fmaxf(mx, ml[j].x);
+    const float corr = __builtin_amdgcn_exp2f(M - mx);  // first batch: M = -inf -> 0
+    L = L * corr;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) A[d] = A[d] * corr;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const float w = __builtin_amdgcn_exp2f(ml[j].x - mx);  // masked slot: exp2(-inf) = 0
+      L = __builtin_fmaf(ml[j].y, w, L);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t x0 = elem(a0[j], d), x1 = elem(a1[j], d);
+        A[d] = __builtin_fmaf(__builtin_bit_cast(float, x0), w, A[d]);
+        A[d + 4] = __builtin_fmaf(__builtin_bit_cast(float, x1), w, A[d + 4]);
+      }
+    }
+    M = mx;
+  }
+  store_out(out, seq, h, n_heads, A, L);
+}
+
+// Merge for many pieces per sequence (the small-batch grid's short runs). Grid
+// (ceil(n_heads / 4), n_seq), 256 threads: wave w merges the pieces of query head
 // 4 * blockIdx.x + w of sequence blockIdx.y, for every sequence that has more than one.
 // pages_per_split > 0: the sequence-split grid's layout, pieces = ceil(P / pages_per_split),
 // empty sequences already written. 0: the page-balanced layout, the piece count read from the
 // sequence's last slot. Lane (sg = lane / 16, dq = lane % 16) folds pieces sg, sg + 4, ... for
-// dims 4 dq .. 4 dq + 3; all of a round's loads (32 pieces per wave) are issued together, so a
-// sequence of up to 32 pieces costs one round trip. The four piece groups then meet in two
-// exchanges across rows. The running maximum M is shared by the whole wave, so every lane's
-// partial sums carry the same scale.
+// dims 4 dq .. 4 dq + 3, 32 pieces per wave per round. The first round is loaded together with
+// the length and the piece count, before the count is known (slots past the count lie inside
+// the workspace and are masked afterwards), so up to 32 pieces cost one round trip. The four
+// piece groups then meet in two exchanges across rows. The running maximum M is shared by the
+// whole wave, so every lane's partial sums carry the same scale. (With ~4 pieces per sequence,
+// as the page-balanced grid leaves at 256 sequences, this layout was 2 us slower per launch
+// than k_attn_merge; with 10-30, as the short runs leave, 8 us faster.)
 constexpr int kMergePer = 8;  // pieces per lane per round
 
 __device__ __forceinline__ void store_nan4(f16* __restrict__ out, int seq, int h, int n_heads,
@@ -576,15 +668,39 @@ __device__ __forceinline__ void store_nan4(f16* __restrict__ out, int seq, int h
 }
 
 __global__ void __launch_bounds__(256)
-k_attn_merge(const float* __restrict__ part_o, const float2* __restrict__ part_ml,
-             const int* __restrict__ seq_lens, f16* __restrict__ out, int max_pages, int n_heads,
-             int num_splits, int pages_per_split) {
+k_attn_merge_many(const float* __restrict__ part_o, const float2* __restrict__ part_ml,
+                  const int* __restrict__ seq_lens, f16* __restrict__ out, int max_pages,
+                  int n_heads, int num_splits, int pages_per_split) {
   const int seq = blockIdx.y;
   const int h = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (h >= n_heads) return;
   const int lane = threadIdx.x & 63, sg = lane >> 4, dq = lane & 15;
   const size_t base = (size_t)seq * num_splits * n_heads + h;  // slot of piece 0
+  float2 ml[kMergePer];
+  float4 a[kMergePer];
+  // Loads the pieces s0 + sg + 4 j in [from, to) of the round starting at s0.
+  auto load_round = [&](int s0, int from, int to) {
+#pragma unroll
+    for (int j = 0; j < kMergePer; ++j) {
+      const int piece = s0 + sg + 4 * j;
+      if (piece >= from && piece < to) {
+        const size_t k = base + (size_t)piece * n_heads;
+        ml[j] = part_ml[k];
+        a[j] = *reinterpret_cast<const float4*>(part_o + k * kHeadDim + 4 * dq);
+      }
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < kMergePer; ++j) {
+    ml[j] = make_float2(-INFINITY, 0.0f);  // no piece: weight exp2(-inf) = 0
+    a[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  const int spec_end = 4 * kMergePer < num_splits ? 4 * kMergePer : num_splits;
+  load_round(0, 0, spec_end);
   const int S = seq_lens[seq];
+  const float2 meta =
+      pages_per_split > 0 ? make_float2(0.0f, 0.0f)
+                          : part_ml[((size_t)seq * num_splits + num_splits - 1) * n_heads];
   const int P = seq_pages(S, max_pages);
   int used;
   if (pages_per_split > 0) {
@@ -594,25 +710,25 @@ k_attn_merge(const float* __restrict__ part_o, const float2* __restrict__ part_m
       if (sg == 0) store_nan4(out, seq, h, n_heads, dq);
       return;
     }
-    used = __builtin_bit_cast(
-        int, part_ml[((size_t)seq * num_splits + num_splits - 1) * n_heads].x);
+    used = __builtin_bit_cast(int, meta.x);
   }
   if (used <= 1) return;
   float M = -INFINITY, L = 0.0f, A[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int s0 = 0; s0 < used; s0 += 4 * kMergePer) {
-    float2 ml[kMergePer];
-    float4 a[kMergePer];
+    if (s0 > 0) {
 #pragma unroll
-    for (int j = 0; j < kMergePer; ++j) {
-      const int piece = s0 + sg + 4 * j;
-      const size_t k = base + (size_t)piece * n_heads;
-      ml[j] = make_float2(-INFINITY, 0.0f);  // no piece: weight exp2(-inf) = 0
-      a[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (piece < used) {
-        ml[j] = part_ml[k];
-        a[j] = *reinterpret_cast<const float4*>(part_o + k * kHeadDim + 4 * dq);
+      for (int j = 0; j < kMergePer; ++j) {
+        ml[j] = make_float2(-INFINITY, 0.0f);
+        a[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
     }
+    load_round(s0, s0 > 0 ? s0 : spec_end, used);
+#pragma unroll
+    for (int j = 0; j < kMergePer; ++j)
+      if (s0 + sg + 4 * j >= used) {  // a slot past the count (may hold NaN): weight 0, no data
+        ml[j] = make_float2(-INFINITY, 0.0f);
+        a[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     float mx = M;
 #pragma unroll
     for (int j = 0; j < kMergePer; ++j) mx = fmaxf(mx, ml[j].x);
@@ -720,7 +836,7 @@ int attn_launch(const AttnArgs& a, hipStream_t s) {
                     0, s, a.q, a.k_pool, a.v_pool, a.tables, a.lens, a.out, a.part_o, a.part_ml,
                     a.n_seq, a.max_pages, a.n_heads, a.n_kv_heads, a.num_splits);
     if (st != 0) return st;
-    const dim3 mgrid((unsigned)((a.n_heads + 3) / 4), (unsigned)a.n_seq);
+    const dim3 mgrid((unsigned)((a.n_heads + 31) / 32), (unsigned)a.n_seq);
     return launch(k_attn_merge, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,
                   a.max_pages, a.n_heads, a.num_splits, 0);
   }
@@ -735,7 +851,12 @@ int attn_launch(const AttnArgs& a, hipStream_t s) {
     st = split_launch<KVW, 0>(a, groups, pps, s);
   }
   if (st != 0 || pps >= a.max_pages) return st;  // every sequence fits in one split
-  const dim3 mgrid((unsigned)((a.n_heads + 3) / 4), (unsigned)a.n_seq);
+  if (short_runs) {
+    const dim3 mgrid((unsigned)((a.n_heads + 3) / 4), (unsigned)a.n_seq);
+    return launch(k_attn_merge_many, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,
+                  a.max_pages, a.n_heads, a.num_splits, pps);
+  }
+  const dim3 mgrid((unsigned)((a.n_heads + 31) / 32), (unsigned)a.n_seq);
   return launch(k_attn_merge, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,
                 a.max_pages, a.n_heads, a.num_splits, pps);
 }
