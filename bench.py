@@ -95,8 +95,9 @@ PROFILE_SHAPES = [
     # 512 blocks: two resident blocks of 256 threads on each of the 256 CUs (191 VGPRs).
     ("attention_decode_256", "k_attn_balancedILi8E", 512 * 256, ATTN_BYTES_256,
      ("k_attn_merge", 256 * 256)),
-    ("attention_decode_16x2048", "k_attn_balancedILi8E", 512 * 256, ATTN_BYTES_16x2048,
-     ("k_attn_merge", 256 * 16)),
+    # 16 sequences take the sequence-split grid (32 splits of 4 pages, 16 blocks per split).
+    ("attention_decode_16x2048", "k_attn_splitILi8ELi0E", 32 * 256 * 16, ATTN_BYTES_16x2048,
+     ("k_attn_merge_many", 8 * 256 * 16)),
     ("argmax_256x128256", "k_argmax_vec", 256 * 1024, 256 * 128256 * 2 + 256 * 4),
     ("decode:embedding_256", "k_embeddingILi0E", 256 * 64, 2098176),
     ("decode:add_rmsnorm_256x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 256 * 64, 4198400),
