@@ -136,8 +136,22 @@ def test_linear_rows_fused_give_the_bits_of_the_separate_launches(llmk, orc, T):
     torch.cuda.synchronize()
     assert np.array_equal(host(y1), host(y2)) and np.array_equal(host(y3), host(y4))
 
-    # residual-add epilogue (in = 8192, 16 waves per block for T <= 4)
+    # norm prologue over in = 8192: one block of 16 waves, the raw slices of all T rows staged
+    # in LDS (135 KB at T = 8)
     K = 8192
+    xk = dev(normal_f16(rng, (T, K)))
+    nwk = dev(normal_f16(rng, (K,), 1.0, 0.1))
+    normed_k = torch.empty(T * K, dtype=torch.float16, device=DEV)
+    llmk.rmsnorm(xk, nwk, normed_k, T, K, eps)
+    wk = dev(normal_f16(rng, (N, K), std=0.02))
+    z1 = torch.full((T * N,), float("nan"), dtype=torch.float16, device=DEV)
+    z2 = z1.clone()
+    llmk.linear_rows_norm(xk, nwk, eps, wk, z1, T, K, N)
+    llmk.linear_rows(normed_k, wk, z2, T, K, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(z1), host(z2))
+
+    # residual-add epilogue (in = 8192, 16 waves per block)
     a = dev(normal_f16(rng, (T, K)))
     wd = dev(normal_f16(rng, (H, K), std=0.02))
     r1 = dev(normal_f16(rng, (T, H)))
