@@ -64,12 +64,14 @@ k_argmax_vec(const f16* __restrict__ logits, int* __restrict__ out, int vocab) {
   float best = -INFINITY;
   int best_i = INT_MAX;
   for (int base = 0; base < nvec; base += kArgmaxUnroll * kArgmaxThreads) {
+    // Vectors past the row's end load its last vector again and compare as -inf: the loads
+    // stay unconditional, so the compares of vector u wait only for load u (with a masked load
+    // the compiler waited for all 16 first; 14.1 -> 13.3 us at [256, 128256]).
     u32x4 x[kArgmaxUnroll];
 #pragma unroll
     for (int u = 0; u < kArgmaxUnroll; ++u) {
       const int j = base + u * kArgmaxThreads + (int)threadIdx.x;
-      const u32x4 none = {0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u};  // -inf
-      x[u] = j < nvec ? ld16_stream(row + (size_t)j * 8) : none;
+      x[u] = ld16_stream(row + (size_t)(j < nvec ? j : nvec - 1) * 8);
     }
 #pragma unroll
     for (int u = 0; u < kArgmaxUnroll; ++u) {
@@ -77,7 +79,7 @@ k_argmax_vec(const f16* __restrict__ logits, int* __restrict__ out, int vocab) {
       const f16x8 h = as_h8(x[u]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float v = (float)h[e];
+        const float v = j < nvec ? (float)h[e] : -INFINITY;
         if (v > best) {  // increasing index within the thread: ties keep the earlier one
           best = v;
           best_i = j * 8 + e;
