@@ -100,34 +100,66 @@ k_rope_vec(f16* q, const f16* k, const f16* __restrict__ v, f16* k_out, f16* v_p
   const f16* vb = FUSED ? v + (size_t)t0 * kvdim : nullptr;
 
   u32x4 x[TASKS];
+  if constexpr (FUSED) {
+    // Fused (decode-sized) launches: the (cos, sin) inputs of the thread's first (token, pair)
+    // and the position of its token's pool row are loaded first; then the data loads, all
+    // unconditional (a vector past the block's runs loads the last one again and is not
+    // stored). Memory waits are in issue order, so the sincos and the page-table lookup
+    // proceed while the data is in flight; with conditional data loads in front, each waited
+    // for all of them.
+    const int cs_n = ntok * HALF;
+    const int e0 = (int)threadIdx.x < cs_n ? (int)threadIdx.x : 0;
+    const int pos0 = pos[t0 + e0 / HALF];
+    const float freq0 = inv_freq[e0 % HALF];
+    const int tr = (int)threadIdx.x < ntok ? (int)threadIdx.x : 0;  // the pool row's token
+    const int prow = pos[t0 + tr];
 #pragma unroll
-  for (int m = 0; m < TASKS; ++m) {
-    const int e = threadIdx.x + m * blockDim.x;
-    if (STRIDED) {
-      // vector e of the concatenated runs -> (token, column) of its strided source row
-      const bool isq = e < qv;
-      const int r = isq ? e : (e < qv + kv ? e - qv : e - qv - kv);
-      const FastDiv dv = isq ? qdiv : kdiv;
-      const int tt = (int)fdiv((uint32_t)r, dv);
-      const int col = r - tt * (int)dv.d;
-      const f16* src = isq ? q_src : (e < qv + kv ? k : v);
-      x[m] = e < total ? ld16_stream(src + (size_t)(t0 + tt) * ld + 8 * col) : u32x4{0, 0, 0, 0};
-    } else {
+    for (int m = 0; m < TASKS; ++m) {
+      const int e = min((int)threadIdx.x + m * (int)blockDim.x, total - 1);
+      if (STRIDED) {
+        // vector e of the concatenated runs -> (token, column) of its strided source row
+        const bool isq = e < qv;
+        const int r = isq ? e : (e < qv + kv ? e - qv : e - qv - kv);
+        const FastDiv dv = isq ? qdiv : kdiv;
+        const int tt = (int)fdiv((uint32_t)r, dv);
+        const int col = r - tt * (int)dv.d;
+        const f16* src = isq ? q_src : (e < qv + kv ? k : v);
+        x[m] = ld16_stream(src + (size_t)(t0 + tt) * ld + 8 * col);
+      } else {
+        const f16* src =
+            e < qv ? qb + 8 * e : (e < qv + kv ? kb + 8 * (e - qv) : vb + 8 * (e - qv - kv));
+        x[m] = ld16_stream(src);
+      }
+    }
+    const int page = tables[(size_t)(t0 + tr) * max_pages + prow / page_size];
+    if ((int)threadIdx.x < cs_n) {
+      const int tt = threadIdx.x / HALF, i = threadIdx.x % HALF;
+      cos_sin_f16((float)pos0 * freq0, cs + tt * HD + i, cs + tt * HD + HALF + i);
+    }
+    for (int e = threadIdx.x + blockDim.x; e < cs_n; e += blockDim.x) {
+      const int tt = e / HALF, i = e % HALF;
+      cos_sin_f16((float)pos[t0 + tt] * inv_freq[i], cs + tt * HD + i, cs + tt * HD + HALF + i);
+    }
+    if ((int)threadIdx.x < ntok) pool_row[tr] = (long long)page * page_size + prow % page_size;
+    for (int tt = threadIdx.x + blockDim.x; tt < ntok; tt += blockDim.x) {
+      const int b = t0 + tt, p = pos[b];
+      const int pg = tables[(size_t)b * max_pages + p / page_size];
+      pool_row[tt] = (long long)pg * page_size + p % page_size;
+    }
+  } else {
+    // Standalone launches (many tokens per block, many blocks): the data loads go first, the
+    // positions after them. (Issuing the positions first, as above, measured 0.5 us slower at
+    // 8192 tokens; at 256 tokens, fused, it is 0.25 us faster.)
+#pragma unroll
+    for (int m = 0; m < TASKS; ++m) {
+      const int e = threadIdx.x + m * blockDim.x;
       if (e < qv) x[m] = ld16_stream(qb + 8 * e);
       else if (e < qv + kv) x[m] = ld16_stream(kb + 8 * (e - qv));
-      else if (FUSED && e < total) x[m] = ld16_stream(vb + 8 * (e - qv - kv));
       else x[m] = u32x4{0, 0, 0, 0};
     }
-  }
-  for (int e = threadIdx.x; e < ntok * HALF; e += blockDim.x) {
-    const int tt = e / HALF, i = e % HALF;
-    cos_sin_f16((float)pos[t0 + tt] * inv_freq[i], cs + tt * HD + i, cs + tt * HD + HALF + i);
-  }
-  if (FUSED) {
-    for (int tt = threadIdx.x; tt < ntok; tt += blockDim.x) {
-      const int b = t0 + tt, p = pos[b];
-      const int page = tables[(size_t)b * max_pages + p / page_size];
-      pool_row[tt] = (long long)page * page_size + p % page_size;
+    for (int e = threadIdx.x; e < ntok * HALF; e += blockDim.x) {
+      const int tt = e / HALF, i = e % HALF;
+      cos_sin_f16((float)pos[t0 + tt] * inv_freq[i], cs + tt * HD + i, cs + tt * HD + HALF + i);
     }
   }
   __syncthreads();
@@ -227,6 +259,7 @@ static int rope_vec_launch(f16* q, const f16* k, const f16* v, f16* k_out, f16* 
     if (tasks <= 2) LLMK_ROPE_LAUNCH(H, 2);  \
     if (tasks <= 4) LLMK_ROPE_LAUNCH(H, 4);  \
     if (tasks <= 8) LLMK_ROPE_LAUNCH(H, 8);  \
+    if (tasks <= 10) LLMK_ROPE_LAUNCH(H, 10); \
     if (tasks <= 12) LLMK_ROPE_LAUNCH(H, 12); \
     LLMK_ROPE_LAUNCH(H, 16);
   switch (hv) {
