@@ -29,8 +29,8 @@ __device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
   }
 }
 
-// Block-wide reduction of (value, index); thread 0 gets the result.
-__device__ __forceinline__ void block_best(float& v, int& i) {
+// Block-wide reduction of (value, index) over the block's nw waves; thread 0 gets the result.
+__device__ __forceinline__ void block_best(float& v, int& i, int nw) {
   __shared__ float sv[kArgmaxWaves];
   __shared__ int si[kArgmaxWaves];
   for (int o = 32; o > 0; o >>= 1) {
@@ -45,7 +45,6 @@ __device__ __forceinline__ void block_best(float& v, int& i) {
   }
   __syncthreads();
   if (wave == 0) {
-    const int nw = (int)blockDim.x >> 6;
     v = lane < nw ? sv[lane] : -INFINITY;
     i = lane < nw ? si[lane] : INT_MAX;
     for (int o = 32; o > 0; o >>= 1) {
@@ -87,7 +86,7 @@ k_argmax_vec(const f16* __restrict__ logits, int* __restrict__ out, int vocab) {
       }
     }
   }
-  block_best(best, best_i);
+  block_best(best, best_i, kArgmaxWaves);
   if (threadIdx.x == 0) out[blockIdx.x] = best_i;
 }
 
@@ -104,7 +103,7 @@ k_argmax_scalar(const f16* __restrict__ logits, int* __restrict__ out, int vocab
       best_i = i;
     }
   }
-  block_best(best, best_i);
+  block_best(best, best_i, (int)blockDim.x >> 6);
   if (threadIdx.x == 0) out[blockIdx.x] = best_i;
 }
 

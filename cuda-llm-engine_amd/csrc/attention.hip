@@ -474,7 +474,7 @@ k_attn_balanced(const f16* __restrict__ q, const f16* __restrict__ k_pool,
                 const f16* __restrict__ v_pool, const int* __restrict__ block_tables,
                 const int* __restrict__ seq_lens, f16* __restrict__ out,
                 float* __restrict__ part_o, float2* __restrict__ part_ml, int n_seq,
-                int max_pages, int n_heads, int n_kv_heads, int num_splits) {
+                int max_pages, int n_heads, int n_kv_heads, int num_splits, int n_blocks) {
   __shared__ MergeLds<KVW> lds;
   __shared__ int red[2 * kWaves];
   __shared__ int found[2];
@@ -499,7 +499,7 @@ k_attn_balanced(const f16* __restrict__ q, const f16* __restrict__ k_pool,
     }
   int T, P_max;
   block_sum_max(mine, red, &T, &P_max);
-  const int per = (T + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int per = (T + n_blocks - 1) / n_blocks;  // n_blocks == gridDim.x, passed in SGPRs
   const int q_min = P_max > 1 ? (P_max - 1 + num_splits - 3) / (num_splits - 2) : 1;
   const int qp = per > q_min ? per : q_min;
   const long long g0l = (long long)b * qp;
@@ -834,7 +834,7 @@ int attn_launch(const AttnArgs& a, hipStream_t s) {
     if (blocks < 1) blocks = 1;
     int st = launch(k_attn_balanced<KVW>, dim3((unsigned)blocks, (unsigned)groups), dim3(kThreads),
                     0, s, a.q, a.k_pool, a.v_pool, a.tables, a.lens, a.out, a.part_o, a.part_ml,
-                    a.n_seq, a.max_pages, a.n_heads, a.n_kv_heads, a.num_splits);
+                    a.n_seq, a.max_pages, a.n_heads, a.n_kv_heads, a.num_splits, blocks);
     if (st != 0) return st;
     const dim3 mgrid((unsigned)((a.n_heads + 31) / 32), (unsigned)a.n_seq);
     return launch(k_attn_merge, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,

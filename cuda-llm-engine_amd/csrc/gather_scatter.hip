@@ -45,15 +45,17 @@ __device__ __forceinline__ void copy_row_kind(const f16* __restrict__ src, f16* 
   else copy_row<4, false>(src, dst, vpr, lane);
 }
 
-__device__ __forceinline__ int wave_row() {
-  return __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+// The wave's row; wpb (waves per block) comes as a kernel argument, not from blockDim: the
+// arguments arrive preloaded in SGPRs, blockDim would cost a scalar fetch first.
+__device__ __forceinline__ int wave_row(int wpb) {
+  return __builtin_amdgcn_readfirstlane(blockIdx.x * wpb + (threadIdx.x >> 6));
 }
 
 template <int KIND>
 __global__ void __launch_bounds__(256)
 k_embedding(const f16* __restrict__ table, const int* __restrict__ ids, f16* __restrict__ out,
-            int n_tokens, int vpr) {
-  const int row = wave_row();
+            int n_tokens, int vpr, int wpb) {
+  const int row = wave_row(wpb);
   if (row >= n_tokens) return;
   const long long id = ids[row];
   copy_row_kind<KIND>(table + id * vpr * 8, out + (size_t)row * vpr * 8, vpr, threadIdx.x & 63);
@@ -67,11 +69,10 @@ k_embedding(const f16* __restrict__ table, const int* __restrict__ ids, f16* __r
 template <int R>
 __global__ void __launch_bounds__(256)
 k_embedding_rows(const f16* __restrict__ table, const int* __restrict__ ids,
-                 f16* __restrict__ out, int n_tokens, int vpr) {
+                 f16* __restrict__ out, int n_tokens, int vpr, int n_waves) {
   const int lane = threadIdx.x & 63;
   const int n_groups = (n_tokens + R - 1) / R;
-  const int n_waves = gridDim.x * (blockDim.x >> 6);
-  for (int g = wave_row(); g < n_groups; g += n_waves) {
+  for (int g = wave_row(4); g < n_groups; g += n_waves) {
     const int row0 = g * R;
     const int my_id = lane < R && row0 + lane < n_tokens ? ids[row0 + lane] : 0;
     long long off[R];  // offsets, not pointers: loads index the restrict-qualified table
@@ -107,8 +108,8 @@ template <bool BATCH, int KIND>
 __global__ void __launch_bounds__(256)
 k_kv_scatter(const f16* __restrict__ src, f16* __restrict__ pool, const int* __restrict__ tables,
              const int* __restrict__ positions, int start_pos, int n_rows, int max_pages,
-             int page_size, int vpr) {
-  const int row = wave_row();
+             int page_size, int vpr, int wpb) {
+  const int row = wave_row(wpb);
   if (row >= n_rows) return;
   const int p = BATCH ? positions[row] : start_pos + row;
   const int* table = BATCH ? tables + (size_t)row * max_pages : tables;
@@ -161,7 +162,7 @@ extern "C" int llmk_embedding_lookup(const uint16_t* table, const int32_t* ids, 
     auto go = [&](auto kern) {
       return launch(kern, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                     reinterpret_cast<const f16*>(table), ids, reinterpret_cast<f16*>(out),
-                    n_tokens, vpr);
+                    n_tokens, vpr, (int)(4 * blocks));
     };
     if (R == 8) return go(k_embedding_rows<8>);
     if (R == 4) return go(k_embedding_rows<4>);
@@ -172,7 +173,7 @@ extern "C" int llmk_embedding_lookup(const uint16_t* table, const int32_t* ids, 
   auto go = [&](auto kern) {
     return launch(kern, grid, dim3(64 * wpb), 0, static_cast<hipStream_t>(stream),
                   reinterpret_cast<const f16*>(table), ids, reinterpret_cast<f16*>(out), n_tokens,
-                  vpr);
+                  vpr, wpb);
   };
   switch (row_kind(vpr)) {
     case 0: return go(k_embedding<0>);
@@ -191,7 +192,7 @@ static int scatter_launch(const uint16_t* src, uint16_t* pool, const int32_t* ta
   auto go = [&](auto kern) {
     return launch(kern, grid, dim3(64 * wpb), 0, static_cast<hipStream_t>(stream),
                   reinterpret_cast<const f16*>(src), reinterpret_cast<f16*>(pool), tables,
-                  positions, start_pos, n_rows, max_pages, page_size, vpr);
+                  positions, start_pos, n_rows, max_pages, page_size, vpr, wpb);
   };
   switch (row_kind(vpr)) {
     case 0: return go(k_kv_scatter<BATCH, 0>);

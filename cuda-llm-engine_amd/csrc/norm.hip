@@ -49,9 +49,11 @@ k_residual_add_scalar(const f16* a, const f16* b, f16* out, size_t n) {
 template <int VPL, bool FUSED, bool FULL>
 __global__ void __launch_bounds__(256)
 k_rmsnorm_wave(const f16* x, f16* resid, const f16* __restrict__ w, f16* out, int n_rows,
-               int vpr, float hidden_f, float eps) {
+               int vpr, float hidden_f, float eps, int wpb) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  // wpb (waves per block) is an argument, not blockDim: the arguments arrive preloaded in
+  // SGPRs, blockDim would cost a scalar fetch before the first address is known.
+  const int row = blockIdx.x * wpb + (threadIdx.x >> 6);
   if (row >= n_rows) return;  // uniform per wave
   const size_t base = (size_t)row * vpr * 8;
   auto owned = [&](int v) { return FULL || v < vpr; };
@@ -148,9 +150,9 @@ static int rmsnorm_launch(const f16* x, f16* resid, const f16* w, f16* out, int 
   const dim3 grid(ceil_div((size_t)n_rows, (size_t)wpb)), block(64 * wpb);
 #define LLMK_NORM_CASE(V)                                                                     \
   return vpr == 64 * V ? launch(k_rmsnorm_wave<V, FUSED, true>, grid, block, 0, stream, x, resid, \
-                                w, out, n_rows, vpr, hf, eps)                                    \
+                                w, out, n_rows, vpr, hf, eps, wpb)                               \
                        : launch(k_rmsnorm_wave<V, FUSED, false>, grid, block, 0, stream, x,      \
-                                resid, w, out, n_rows, vpr, hf, eps)
+                                resid, w, out, n_rows, vpr, hf, eps, wpb)
   if (vpl <= 1) LLMK_NORM_CASE(1);
   if (vpl <= 2) LLMK_NORM_CASE(2);
   if (vpl <= 4) LLMK_NORM_CASE(4);

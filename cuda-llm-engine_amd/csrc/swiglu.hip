@@ -57,6 +57,10 @@ __device__ __forceinline__ void silu_vectors(const u32x4 (&g)[NV], u32x4 (&s)[NV
 // range in one pass. Blocks wholly inside the range take a straight-line path without
 // per-vector tests, so all 2 * UNROLL loads issue back to back; only the last block tests.
 // (A grid-stride loop around the same body measured 10% slower at [8192, 8192].)
+// Threads per block of the vector kernels (a constant, not blockDim: the kernel arguments
+// arrive preloaded in SGPRs, blockDim would cost a scalar fetch before the first address).
+constexpr int kSwigluThreads = 256;
+
 template <int UNROLL>
 __device__ __forceinline__ void swiglu_block(const f16* __restrict__ gate, const f16* __restrict__ up,
                                              f16* __restrict__ out, size_t b, size_t nvec,
@@ -65,7 +69,7 @@ __device__ __forceinline__ void swiglu_block(const f16* __restrict__ gate, const
   const u32x4 ones = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
 #pragma unroll
   for (int m = 0; m < UNROLL; ++m) {
-    const size_t i = b + threadIdx.x + (size_t)m * blockDim.x;
+    const size_t i = b + threadIdx.x + (size_t)m * kSwigluThreads;
     // Past the end: gate 1.0 (a value the fast path settles); nothing is stored there.
     g[m] = whole || i < nvec ? ld16_stream(gate + 8 * i) : ones;
     u[m] = whole || i < nvec ? ld16_stream(up + 8 * i) : ones;
@@ -73,20 +77,20 @@ __device__ __forceinline__ void swiglu_block(const f16* __restrict__ gate, const
   silu_vectors<UNROLL>(g, sv);
 #pragma unroll
   for (int m = 0; m < UNROLL; ++m) {
-    const size_t i = b + threadIdx.x + (size_t)m * blockDim.x;
+    const size_t i = b + threadIdx.x + (size_t)m * kSwigluThreads;
     if (whole || i < nvec) st16_stream(out + 8 * i, as_u4(as_h8(sv[m]) * as_h8(u[m])));
   }
 }
 
 template <int UNROLL>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kSwigluThreads)
 k_swiglu_vec(const f16* __restrict__ gate, const f16* __restrict__ up, f16* __restrict__ out,
              size_t nvec, size_t n) {
-  const size_t chunk = (size_t)blockDim.x * UNROLL;
+  const size_t chunk = (size_t)kSwigluThreads * UNROLL;
   const size_t b = (size_t)blockIdx.x * chunk;
   if (b + chunk <= nvec) swiglu_block<UNROLL>(gate, up, out, b, nvec, true);
   else if (b < nvec) swiglu_block<UNROLL>(gate, up, out, b, nvec, false);
-  const size_t t = nvec * 8 + (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // n % 8 tail
+  const size_t t = nvec * 8 + (size_t)blockIdx.x * kSwigluThreads + threadIdx.x;  // n % 8 tail
   if (t < n) out[t] = silu_r16(gate[t]) * up[t];
 }
 
@@ -102,12 +106,12 @@ k_swiglu_scalar(const f16* __restrict__ gate, const f16* __restrict__ up, f16* _
 // in [inter, 2 * inter); out row r = swiglu(gate row, up row). Grid (column blocks, rows), the
 // same per-block body as the flat kernel over each row's two runs.
 template <int UNROLL>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kSwigluThreads)
 k_swiglu_rows(const f16* __restrict__ gu, f16* __restrict__ out, int inter) {
   const size_t r = blockIdx.y;
   const f16* g = gu + r * 2 * (size_t)inter;
   const size_t nvec = (size_t)inter / 8;
-  const size_t chunk = (size_t)blockDim.x * UNROLL;
+  const size_t chunk = (size_t)kSwigluThreads * UNROLL;
   const size_t b = (size_t)blockIdx.x * chunk;
   if (b + chunk <= nvec) swiglu_block<UNROLL>(g, g + inter, out + r * inter, b, nvec, true);
   else if (b < nvec) swiglu_block<UNROLL>(g, g + inter, out + r * inter, b, nvec, false);
@@ -126,8 +130,9 @@ extern "C" int llmk_swiglu_rows(const uint16_t* gate_up, uint16_t* out, int n_ro
   if (n_rows > 65535) return LLMK_ERR_UNSUPPORTED;
   if (!aligned16(gate_up) || !aligned16(out)) return LLMK_ERR_ALIGNMENT;
   constexpr int UNROLL = 2;
-  const dim3 grid(ceil_div((size_t)inter / 8, 256 * UNROLL), (unsigned)n_rows);
-  return launch(k_swiglu_rows<UNROLL>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+  const dim3 grid(ceil_div((size_t)inter / 8, kSwigluThreads * UNROLL), (unsigned)n_rows);
+  return launch(k_swiglu_rows<UNROLL>, grid, dim3(kSwigluThreads), 0,
+                static_cast<hipStream_t>(stream),
                 reinterpret_cast<const f16*>(gate_up), reinterpret_cast<f16*>(out), inter);
 }
 
@@ -143,10 +148,12 @@ extern "C" int llmk_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* o
     // One pass over the range: each thread owns UNROLL vectors of each input.
     constexpr int UNROLL = 2;
     const size_t nvec = n / 8;
-    const size_t need = ((nvec > 0 ? nvec : 1) + 256 * UNROLL - 1) / (256 * UNROLL);
+    const size_t need =
+        ((nvec > 0 ? nvec : 1) + kSwigluThreads * UNROLL - 1) / (kSwigluThreads * UNROLL);
     if (need > 0x7FFFFFFFu) return LLMK_ERR_UNSUPPORTED;  // > 2^40 elements
     const unsigned blocks = (unsigned)need;
-    return launch(k_swiglu_vec<UNROLL>, dim3(blocks), dim3(256), 0, s, g, u, o, nvec, n);
+    return launch(k_swiglu_vec<UNROLL>, dim3(blocks), dim3(kSwigluThreads), 0, s, g, u, o, nvec,
+                  n);
   }
   const unsigned blocks = ceil_div(n, 256) < 8192u ? ceil_div(n, 256) : 8192u;
   return launch(k_swiglu_scalar, dim3(blocks), dim3(256), 0, s, g, u, o, n);
