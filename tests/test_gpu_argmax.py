@@ -85,3 +85,31 @@ def test_zero_rows_and_bad_arguments(llmk):
         llmk.argmax_rows(t, out, 1, 0)
     with pytest.raises(llmk.LlmkError):
         llmk.argmax_rows(t, out, 2, 16)  # logits too short
+
+
+@pytest.mark.parametrize("vocab", [8200, 32008, V, 131080])
+def test_maxima_in_the_last_vector(llmk, orc, vocab):
+    """Past the row's end the 16-byte kernel reloads the last vector instead of masking, so a
+    copy of it shows up at indices >= vocab: every maximum placed in that vector must still
+    come back at its own index (8200 and 32008 leave thousands of copies; 131080 needs a second
+    pass over the row)."""
+    rng = np.random.default_rng(vocab)
+    rows = rng.uniform(-3, 3, (8, vocab)).astype(np.float16)
+    nan, inf = np.float16(np.nan), np.float16(np.inf)
+    rows[0, vocab - 1] = 9                       # last element
+    rows[1, vocab - 8] = 9                       # first element of the last vector
+    rows[2, [vocab - 5, vocab - 1]] = 9          # tie inside the last vector
+    rows[3, [3, vocab - 1]] = 9                  # tie with the start of the row
+    rows[4, :] = nan                             # no value above -inf anywhere
+    rows[4, vocab - 8:] = -inf
+    rows[5, vocab - 8:] = 9                      # the whole last vector ties
+    rows[6, vocab - 8:] = inf
+    rows[6, vocab // 3] = inf                    # +inf earlier in the row wins the tie
+    rows[7, :] = -2
+    rows[7, vocab - 2] = -0.0                    # -0 and +0 tie: the first
+    rows[7, vocab - 1] = 0.0
+    bits = rows.view(np.uint16)
+    got = run(llmk, bits)
+    assert np.array_equal(got, orc.argmax_rows(bits, 8, vocab))
+    assert list(got) == [vocab - 1, vocab - 8, vocab - 5, 3, 0x7FFFFFFF, vocab - 8, vocab // 3,
+                         vocab - 2]
