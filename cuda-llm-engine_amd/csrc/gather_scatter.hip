@@ -9,6 +9,8 @@
 //
 // ref: kernels/embedding.cu:4-16 (embedding_lookup), kernels/kv_scatter.cu:4-40 (kv_scatter,
 // kv_scatter_batch), bench/bandwidth.cu:11-15 (copy probe).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace llmk {
@@ -64,41 +66,70 @@ k_embedding(const f16* __restrict__ table, const int* __restrict__ ids, f16* __r
 // Rows whose width is a multiple of 256 vectors (hidden % 2048 == 0), R rows per wave: for each
 // 256-vector slice, the R rows' loads (4 per lane per row) are all issued before any store, so
 // a wave keeps 16 * 4 * R bytes per lane in flight. Groups of R consecutive tokens are dealt to
-// the waves round-robin; the host sizes the grid at one 4-wave block per CU at most. The R ids
-// of a group arrive with one vector load (lane h reads id h) and are broadcast with readlane.
+// the waves round-robin; the host sizes the grid at one 4-wave block per CU at most.
+// The group's ids are wave-uniform and come through the scalar cache (one s_load_dwordx8 for a
+// full group of 8) instead of one vector load and 8 readlanes. VPR > 0 fixes the row width at
+// compile time (256 vectors = hidden 2048, 512 = hidden 4096): the row bases then stay in scalar
+// registers and each load is base + lane offset, where a runtime width costs a 64-bit VGPR
+// address per load (12.1 -> 11.7 us at 8192 tokens of 2048).
 template <int R>
-__global__ void __launch_bounds__(256)
-k_embedding_rows(const f16* __restrict__ table, const int* __restrict__ ids,
-                 f16* __restrict__ out, int n_tokens, int vpr, int n_waves) {
-  const int lane = threadIdx.x & 63;
-  const int n_groups = (n_tokens + R - 1) / R;
-  for (int g = wave_row(4); g < n_groups; g += n_waves) {
-    const int row0 = g * R;
-    const int my_id = lane < R && row0 + lane < n_tokens ? ids[row0 + lane] : 0;
-    long long off[R];  // offsets, not pointers: loads index the restrict-qualified table
+__device__ __forceinline__ void gather_group(const f16* __restrict__ table,
+                                             const int* __restrict__ ids, f16* __restrict__ out,
+                                             int row0, int n_rows, int vpr, int lane) {
+  long long off[R];  // offsets, not pointers: loads index the restrict-qualified table
+#pragma unroll
+  for (int h = 0; h < R; ++h) {
+    // A partial group (n_rows < R) reads its last id again for the rows it does not store.
+    const int t = h < n_rows ? h : n_rows - 1;
+    off[h] = (long long)__builtin_amdgcn_readfirstlane(ids[row0 + t]) * vpr * 8;
+  }
+  for (int v0 = 0; v0 < vpr; v0 += 256) {
+    u32x4 r[4 * R];
 #pragma unroll
     for (int h = 0; h < R; ++h)
-      off[h] = (long long)__builtin_amdgcn_readlane(my_id, h) * vpr * 8;
-    for (int v0 = 0; v0 < vpr; v0 += 256) {
-      u32x4 r[4 * R];
 #pragma unroll
-      for (int h = 0; h < R; ++h)
+      for (int m = 0; m < 4; ++m)
+        r[4 * h + m] = ld16_stream(table + off[h] + 8 * (v0 + lane + 64 * m));
+    // Keep the scheduler from sinking loads below stores to save registers: the point is to
+    // have all 4 * R loads in flight at once.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          r[4 * h + m] = ld16_stream(table + off[h] + 8 * (v0 + lane + 64 * m));
-      // Keep the scheduler from sinking loads below stores to save registers: the point is to
-      // have all 4 * R loads in flight at once.
-      __builtin_amdgcn_sched_barrier(0);
+    for (int h = 0; h < R; ++h) {
+      if (h < n_rows) {
+        f16* dst = out + (size_t)(row0 + h) * vpr * 8;
 #pragma unroll
-      for (int h = 0; h < R; ++h) {
-        if (row0 + h < n_tokens) {
-          f16* dst = out + (size_t)(row0 + h) * vpr * 8;
-#pragma unroll
-          for (int m = 0; m < 4; ++m) st16_stream(dst + 8 * (v0 + lane + 64 * m), r[4 * h + m]);
-        }
+        for (int m = 0; m < 4; ++m) st16_stream(dst + 8 * (v0 + lane + 64 * m), r[4 * h + m]);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ONE: the grid has a wave for every group (up to 8192 tokens), so no loop (0.1-0.15 us less
+// than the loop's single pass at 8192 tokens).
+template <int R, int VPR, bool ONE>
+__global__ void __launch_bounds__(256)
+k_embedding_rows(const f16* __restrict__ table, const int* __restrict__ ids,
+                 f16* __restrict__ out, int n_tokens, int vpr_arg, int n_waves) {
+  const int vpr = VPR > 0 ? VPR : vpr_arg;
+  const int lane = threadIdx.x & 63;
+  const int n_groups = (n_tokens + R - 1) / R;
+  if (ONE) {
+    const int g = wave_row(4);
+    if (g >= n_groups) return;
+    const int row0 = g * R;
+    if (row0 + R <= n_tokens)
+      gather_group<R>(table, ids, out, row0, R, vpr, lane);
+    else
+      gather_group<R>(table, ids, out, row0, n_tokens - row0, vpr, lane);
+    return;
+  }
+  for (int g = wave_row(4); g < n_groups; g += n_waves) {
+    const int row0 = g * R;
+    if (row0 + R <= n_tokens)
+      gather_group<R>(table, ids, out, row0, R, vpr, lane);  // constant row count: no guards
+    else
+      gather_group<R>(table, ids, out, row0, n_tokens - row0, vpr, lane);
   }
 }
 
@@ -155,7 +186,7 @@ extern "C" int llmk_embedding_lookup(const uint16_t* table, const int32_t* ids, 
   const int vpr = hidden / 8;
   if (vpr % 256 == 0 && n_tokens > 1024) {
     // 1024 waves (4 per CU, one block per CU), each moving R rows at a time: at 8192 tokens of
-    // 2048 this measured 12.0 us against 13.9 us for one row per wave.
+    // 2048 this measured 11.7 us against 13.9 us for one row per wave.
     const int R = n_tokens >= 8 * 1024 ? 8 : (n_tokens >= 4 * 1024 ? 4 : 2);
     const int groups = (n_tokens + R - 1) / R;
     const unsigned blocks = ceil_div((size_t)(groups < 1024 ? groups : 1024), 4);
@@ -164,9 +195,18 @@ extern "C" int llmk_embedding_lookup(const uint16_t* table, const int32_t* ids, 
                     reinterpret_cast<const f16*>(table), ids, reinterpret_cast<f16*>(out),
                     n_tokens, vpr, (int)(4 * blocks));
     };
-    if (R == 8) return go(k_embedding_rows<8>);
-    if (R == 4) return go(k_embedding_rows<4>);
-    return go(k_embedding_rows<2>);
+    const bool one = groups <= (int)(4 * blocks);
+    auto width = [&](auto r) {
+      constexpr int RR = decltype(r)::value;
+      if (vpr == 256)
+        return one ? go(k_embedding_rows<RR, 256, true>) : go(k_embedding_rows<RR, 256, false>);
+      if (vpr == 512)
+        return one ? go(k_embedding_rows<RR, 512, true>) : go(k_embedding_rows<RR, 512, false>);
+      return one ? go(k_embedding_rows<RR, 0, true>) : go(k_embedding_rows<RR, 0, false>);
+    };
+    if (R == 8) return width(std::integral_constant<int, 8>());
+    if (R == 4) return width(std::integral_constant<int, 4>());
+    return width(std::integral_constant<int, 2>());
   }
   int wpb;
   const dim3 grid = rows_grid(n_tokens, &wpb);

@@ -60,6 +60,25 @@ def test_embedding_lookup(llmk, orc, hidden, n):
     assert np.all(got[n] == CANARY)
 
 
+@pytest.mark.parametrize("hidden", [2048, 4096, 6144])
+@pytest.mark.parametrize("n", [1500, 2047, 4096, 8192, 8193])
+def test_embedding_lookup_grouped_rows(llmk, orc, hidden, n):
+    """The many-token kernel (hidden a multiple of 2048, more than 1024 tokens): 2, 4 or 8 rows
+    per wave, one group per wave (n <= 8192) or a loop over groups (8193), a partial last group
+    (1500 with 2 per wave leaves waves without one; 2047 and 8193 end in a part group), and
+    compile-time (2048, 4096) or runtime (6144) row widths."""
+    rng = np.random.default_rng(hidden + n)
+    vocab = 3000
+    table = normal_f16(rng, (vocab, hidden), 0.0, 0.02)
+    ids = rng.integers(0, vocab, n).astype(np.int32)
+    ids[-1] = vocab - 1
+    out = filled((n + 1) * hidden, CANARY)
+    llmk.embedding_lookup(dev(table), dev_i32(ids), out, n, hidden)
+    got = host(out).reshape(n + 1, hidden)
+    assert np.array_equal(got[:n], orc.embedding_lookup(table, ids, hidden))
+    assert np.all(got[n] == CANARY)
+
+
 # --------------------------------------------------------------------------------------------
 def test_residual_add_reference_kat(llmk, orc):
     """ref: tests/test_residual_add.cu:12-58 -- out of place with a canary, then in place."""
