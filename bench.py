@@ -88,7 +88,8 @@ ATTN_BYTES_16x2048 = 67_248_192  # 16 sequences x 2048 positions
 PROFILE_SHAPES = [
     ("add_rmsnorm_8192x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 8192 * 64, 134221824),
     ("rmsnorm_16x2048", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
-    ("rope_8192", "k_rope_vecILi4ELi12ELb0E", 1024 * 256, 83918976),
+    # 8 tokens per block, 10 vector tasks per thread (40 heads x 8 vectors x 8 tokens / 256)
+    ("rope_8192", "k_rope_vecILi4ELi10ELb0E", 1024 * 256, 83918976),
     ("swiglu_8192x8192", "k_swiglu_vecILi2E", 16384 * 256, 402653184),
     ("embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
     ("copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),
@@ -173,16 +174,19 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
     print(f"# write_kib: FETCH_SIZE and WRITE_SIZE per dispatch. traffic_bytes = fetch_kib*1024*"
           f"{sf:.4f} + write_kib*1024*{sw:.4f}, the factors being 1 GiB over what each counter")
     print("# reads for the 1 GiB copy probe (1 GiB read and 1 GiB written per launch).")
+    missing = []
     for label, _, _, alg, *_ in PROFILE_SHAPES:
         d = dur.get(label, [])
         f, w = avg.get((label, "FETCH_SIZE")), avg.get((label, "WRITE_SIZE"))
         us = f"{sum(d) / len(d):.3f}" if d else "-"
-        if f is None or w is None:
-            print(f"{label} us_mean={us} calls={len(d)}")
+        if f is None or w is None or not d:
+            print(f"{label} us_mean={us} calls={len(d)} MISSING (kernel name or grid not found)")
+            missing.append(label)
             continue
         traffic = f * 1024 * sf + w * 1024 * sw
         print(f"{label} us_mean={us} calls={len(d)} fetch_kib={f:.1f} write_kib={w:.1f} "
               f"traffic_bytes={traffic:.0f} algorithmic_bytes={alg} ratio={traffic / alg:.4f}")
+    return 1 if missing else 0
 
 
 def summarize_step(trace_dir, n_rows=256):
@@ -320,8 +324,7 @@ def sets_for(bytes_per_set: int, floor: int = 1 << 30, most: int = 64) -> int:
 def main() -> int:
     args = parse_args()
     if args.summarize_profiles:
-        summarize_profiles(*args.summarize_profiles)
-        return 0
+        return summarize_profiles(*args.summarize_profiles)  # 1 when a launch shape is missing
     if args.summarize_step:
         summarize_step(args.summarize_step[0],
                        int(args.summarize_step[1]) if len(args.summarize_step) > 1 else 256)
