@@ -354,8 +354,10 @@ LLMK_API int llmk_engine_set_rows(llmk_engine* e, int n_rows, const int32_t* tok
 /* Enqueues the forward pass over the first n_rows uploaded rows: embedding, every layer (K and
  * V of each row written to the pools), final norm, logits [nl, vocab] and their argmax [nl]
  * (nl = n_rows if n_logit_rows < 0, else the uploaded logit rows). num_splits <= 0 picks the
- * split count (capped at 32, the workspace). Allocates nothing; capturable into a HIP graph
- * for a fixed n_rows. ref: engine/batched.cu:107-120 (decode_step_gpu), :44-72
+ * split count: 1 when every uploaded row's attention reads at most 4 pages (no merge launch),
+ * else LLMK_ATTN_TARGET_BLOCKS / (n_rows * n_kv_heads) at most max_pages; always capped at 32,
+ * the workspace. Allocates nothing; capturable into a HIP graph for a fixed n_rows (and, with
+ * num_splits <= 0, rows of the same kind: the count is resolved when the pass is enqueued). ref: engine/batched.cu:107-120 (decode_step_gpu), :44-72
  * (layer_forward_batched), :150 (argmax_rows in model_decode_batch_greedy). */
 LLMK_API int llmk_engine_forward(llmk_engine* e, int n_rows, int n_logit_rows, int num_splits,
                                  void* stream);
@@ -385,7 +387,8 @@ LLMK_API int llmk_engine_set_option(llmk_engine* e, int option, int value);
  * Synchronous; not capturable. */
 LLMK_API int llmk_engine_tune(llmk_engine* e, int n_rows, int n_logit_rows, void* stream);
 
-/* llmk_engine_forward through a HIP graph cache keyed by (n_rows, n_logit_rows, num_splits):
+/* llmk_engine_forward through a HIP graph cache keyed by (n_rows, n_logit_rows, the resolved
+ * split count -- num_splits <= 0 resolved against the rows last uploaded, as above):
  * the first call of a key runs eagerly (choosing the GEMM plans), the second captures the pass
  * on `stream` and instantiates it, later calls launch the instance. Same results as
  * llmk_engine_forward. `stream` must not be the null stream (it cannot be captured) and must

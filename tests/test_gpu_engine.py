@@ -437,6 +437,44 @@ def test_engine_fused_few_rows_pass_gives_the_bits_of_the_unfused_pass(llmk, orc
         assert torch.equal(a, b)
 
 
+def test_engine_split_rule_short_contexts_take_one_split(llmk, orc):
+    """num_splits = 0 lets the engine choose: one attention split (no merge launch) when every
+    row's attention spans at most 4 pages, else the reference's rule, target blocks / (rows x kv
+    heads) capped at the table's pages. The automatic pass must give the bits of that explicit
+    split count, eagerly and through the graph cache (first use eager, then captured and
+    replayed: the cache is keyed by the resolved count)."""
+    w = tiny_weights(0x5EED0260, embed_std=0.5, cfg=WIDE)
+    num_pages, max_pages, n = 96, 16, 3
+    e = make_engine(llmk, WIDE, w, 16, max_pages, num_pages)
+    rng = np.random.default_rng(0x5EED0261)
+    tables = rng.permutation(num_pages).astype(np.int32)[:n * max_pages].reshape(n, max_pages)
+    tok = rng.integers(0, WIDE["vocab"], n).astype(np.int32)
+    kvdim = WIDE["n_kv_heads"] * WIDE["head_dim"]
+    fill = torch.randn(num_pages * 16 * kvdim, device=DEV).half()
+    long_rule = min(65536 // (n * WIDE["n_kv_heads"]), max_pages, 32)
+    s = torch.cuda.Stream()
+    for pos, splits in ((np.array([0, 37, 63], np.int32), 1),            # spans 1, 3, 4 pages
+                        (np.array([5, 64, 255], np.int32), long_rule)):  # spans up to 16
+        def run(**kw):
+            for l in range(WIDE["n_layers"]):
+                for which in (llmk.BUF_K_POOL, llmk.BUF_V_POOL):
+                    e.write_pool(which, l, fill)
+            e.set_rows(tok, pos, tables)
+            if kw.pop("graph", False):
+                with torch.cuda.stream(s):
+                    e.forward_graph(n, stream=s, **kw)
+            else:
+                e.forward(n, **kw)
+            torch.cuda.synchronize()
+            return e.logits(n).view(torch.int16).clone()
+
+        explicit = run(num_splits=splits)
+        assert not torch.isnan(explicit.view(torch.float16)).any()
+        assert torch.equal(run(), explicit), (pos, splits)
+        for rep in range(3):  # eager, captured, replayed
+            assert torch.equal(run(graph=True), explicit), (pos, splits, rep)
+
+
 def test_engine_graph_replays_match_eager(llmk, orc):
     w = tiny_weights(0x5EED0240, embed_std=0.5)
     e = make_engine(llmk, TINY, w, 16, 4, 64)
