@@ -57,6 +57,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
                     help="summarise rocprofv3 csv output of this bench instead of running it")
+    ap.add_argument("--summarize-sched", metavar="TRACE_DIR",
+                    help="summarize a rocprofv3 kernel trace of --kernels sched by row count")
     ap.add_argument("--summarize-step", nargs="+", metavar="TRACE_DIR [ROWS]",
                     help="per-kernel time of one engine decode step of ROWS (256) sequences from "
                          "a rocprofv3 kernel trace of `bench.py --kernels step` (or step8, 8)")
@@ -227,6 +229,51 @@ def summarize_step(trace_dir, n_rows=256):
     print(f"# sum of kernel time per step: {total:.1f} us")
 
 
+def summarize_sched(trace_dir, min_passes=20, top=10):
+    """Forward passes of the scheduler workload, grouped by row count: a pass runs from an
+    embedding gather to the next argmax (a gather of logit rows inside the pass is part of it).
+    For every row count with at least min_passes passes: passes, kernel time per pass, and the
+    top kernels (launches per pass, mean duration, time per pass, grid)."""
+    import csv
+    import glob
+    rows = []
+    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+
+    def grid(r):
+        return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+
+    passes, cur = {}, None
+    for r in rows:
+        name = r["Kernel_Name"]
+        if "llmk" not in name and not name.startswith("Cijk"):
+            continue
+        if cur is None:
+            if "k_embedding" not in name:
+                continue
+            cur = {"n": grid(r) // 64, "k": []}
+        cur["k"].append((name, grid(r), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+        if "k_argmax" in name:
+            passes.setdefault(cur["n"], []).append(cur["k"])
+            cur = None
+    print("# engine forward passes of the scheduler workload, by row count")
+    for n in sorted(passes):
+        ps = passes[n]
+        if len(ps) < min_passes:
+            continue
+        agg = {}
+        for p_ in ps:
+            for name, g, d in p_:
+                agg.setdefault((name, g), []).append(d)
+        total = sum(sum(d) for d in agg.values()) / len(ps)
+        print(f"# {n} rows: {len(ps)} passes, kernel time {total:.1f} us per pass")
+        print("# launches/pass  mean_us  us/pass  grid  kernel")
+        for (name, g), d in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:top]:
+            print(f"{len(d) / len(ps):8.2f} {sum(d) / len(d):9.2f} {sum(d) / len(ps):9.1f} "
+                  f"{g:9d}  {name[:100]}")
+
+
 class Timer:
     """Two timed passes of `steps` launches each.
 
@@ -325,6 +372,9 @@ def main() -> int:
     args = parse_args()
     if args.summarize_profiles:
         return summarize_profiles(*args.summarize_profiles)  # 1 when a launch shape is missing
+    if args.summarize_sched:
+        summarize_sched(args.summarize_sched)
+        return 0
     if args.summarize_step:
         summarize_step(args.summarize_step[0],
                        int(args.summarize_step[1]) if len(args.summarize_step) > 1 else 256)
