@@ -90,6 +90,9 @@ struct llmk_engine {
 
   // Pages the longest attention of the rows last set reads (position / 16 + 1).
   int rows_span = 0;
+  // Rows and logit rows uploaded by the last llmk_engine_set_rows: a pass may not ask for more,
+  // since the device copies past them hold no checked indices.
+  int rows_set = 0, logit_rows_set = 0;
 
   // HIP graphs of the forward pass, keyed by (n_rows, n_logit_rows, resolved num_splits)
   struct Graph {
@@ -217,6 +220,7 @@ extern "C" int llmk_engine_create(const llmk_model_config* cfg, int max_rows, in
   if (st == LLMK_OK && cfg->n_layers > 0)
     st = (int)hipMalloc(&e->pool_buf, 2 * (size_t)cfg->n_layers * e->pool_elems * 2);
   if (st == LLMK_OK) st = (int)hipHostMalloc(&e->staging, ci.off, hipHostMallocDefault);
+  if (st == LLMK_OK) memset(e->staging, 0, ci.off);  // every upload copies all of it
   if (st == LLMK_OK) st = (int)hipEventCreateWithFlags(&e->staged, hipEventDisableTiming);
   if (st == LLMK_OK) st = llmk_blas_create(&e->blas);
   if (st != LLMK_OK) {
@@ -427,7 +431,17 @@ extern "C" int llmk_engine_set_rows(llmk_engine* e, int n_rows, const int32_t* t
   hipStream_t s = static_cast<hipStream_t>(stream);
   st = (int)hipMemcpyAsync(e->in_buf, e->staging, e->in_bytes, hipMemcpyHostToDevice, s);
   if (st == LLMK_OK) st = (int)hipEventRecord(e->staged, s);
+  if (st == LLMK_OK) {
+    e->rows_set = n_rows;
+    e->logit_rows_set = n_logit_rows > 0 ? n_logit_rows : 0;
+  }
   return st;
+}
+
+// A pass over n rows with n_logit_rows selected rows (< 0: all rows) reads only row inputs the
+// last llmk_engine_set_rows uploaded and checked.
+static bool rows_uploaded(const llmk_engine* e, int n_rows, int n_logit_rows) {
+  return n_rows <= e->rows_set && n_logit_rows <= e->logit_rows_set;
 }
 
 // Attention splits of a pass over n rows. num_splits <= 0 asks for the engine's choice:
@@ -443,9 +457,11 @@ extern "C" int llmk_engine_set_rows(llmk_engine* e, int n_rows, const int32_t* t
 // rounding; a graph is cached per resolved count, so replays keep their launch shapes.
 constexpr int kOneSplitPages = 4;
 
-static int resolve_splits(const llmk_engine* e, int n, int num_splits) {
+static int resolve_splits(const llmk_engine* e, int n, int num_splits, bool capturing = false) {
   if (num_splits <= 0) {
-    if (e->rows_span <= kOneSplitPages) return 1;
+    // A pass captured by the caller is replayed for rows set later: the short-context rule,
+    // which follows the rows set now, would bake one split into every replay.
+    if (!capturing && e->rows_span <= kOneSplitPages) return 1;
     num_splits = LLMK_ATTN_TARGET_BLOCKS / (n * e->cfg.n_kv_heads);
     if (num_splits > e->max_pages) num_splits = e->max_pages;
     if (num_splits < 1) num_splits = 1;
@@ -531,11 +547,19 @@ extern "C" int llmk_engine_forward(llmk_engine* e, int n_rows, int n_logit_rows,
   if (!e || n_rows < 0 || n_rows > e->max_rows || n_logit_rows > n_rows)
     return LLMK_ERR_INVALID_VALUE;
   if (n_rows == 0) return LLMK_OK;
+  if (!rows_uploaded(e, n_rows, n_logit_rows)) return LLMK_ERR_INVALID_VALUE;
   const llmk_model_config& m = e->cfg;
   const int n = n_rows, H = m.hidden, L = m.n_layers;
   const bool all_rows = n_logit_rows < 0;
   const int nl = all_rows ? n : n_logit_rows;
-  num_splits = resolve_splits(e, n, num_splits);
+  bool capturing = false;
+  if (num_splits <= 0) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const int st = (int)hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap);
+    if (st != LLMK_OK) return st;
+    capturing = cap != hipStreamCaptureStatusNone;
+  }
+  num_splits = resolve_splits(e, n, num_splits, capturing);
   void* s = stream;
   if (fused_rows_path(e, n)) return forward_fused_rows(e, n, nl, all_rows, num_splits, s);
 #define LLMK_TRY(call)               \
@@ -613,6 +637,7 @@ extern "C" int llmk_engine_forward_graph(llmk_engine* e, int n_rows, int n_logit
   if (cap != hipStreamCaptureStatusNone) return LLMK_ERR_INVALID_VALUE;
   if (n_rows < 0 || n_rows > e->max_rows || n_logit_rows > n_rows) return LLMK_ERR_INVALID_VALUE;
   if (n_rows == 0) return LLMK_OK;
+  if (!rows_uploaded(e, n_rows, n_logit_rows)) return LLMK_ERR_INVALID_VALUE;
   num_splits = resolve_splits(e, n_rows, num_splits);  // the key holds the launch shapes
   llmk_engine::Graph& g = e->graphs[std::make_tuple(n_rows, n_logit_rows < 0 ? -1 : n_logit_rows,
                                                     num_splits)];

@@ -353,12 +353,16 @@ LLMK_API int llmk_engine_set_rows(llmk_engine* e, int n_rows, const int32_t* tok
 
 /* Enqueues the forward pass over the first n_rows uploaded rows: embedding, every layer (K and
  * V of each row written to the pools), final norm, logits [nl, vocab] and their argmax [nl]
- * (nl = n_rows if n_logit_rows < 0, else the uploaded logit rows). num_splits <= 0 picks the
- * split count: 1 when every uploaded row's attention reads at most 4 pages (no merge launch),
- * else LLMK_ATTN_TARGET_BLOCKS / (n_rows * n_kv_heads) at most max_pages; always capped at 32,
- * the workspace. Allocates nothing; capturable into a HIP graph for a fixed n_rows (and, with
- * num_splits <= 0, rows of the same kind: the count is resolved when the pass is enqueued). ref: engine/batched.cu:107-120 (decode_step_gpu), :44-72
- * (layer_forward_batched), :150 (argmax_rows in model_decode_batch_greedy). */
+ * (nl = n_rows if n_logit_rows < 0, else the uploaded logit rows). n_rows may not exceed the
+ * rows of the last llmk_engine_set_rows, nor n_logit_rows its logit rows
+ * (LLMK_ERR_INVALID_VALUE before any launch): only those rows' indices were checked.
+ * num_splits <= 0 picks the split count: 1 when every uploaded row's attention reads at most 4
+ * pages (no merge launch), else LLMK_ATTN_TARGET_BLOCKS / (n_rows * n_kv_heads) at most
+ * max_pages; always capped at 32, the workspace. On a stream that is being captured the first
+ * rule is skipped, so that a captured pass keeps enough splits for the longer contexts it may
+ * be replayed with. Allocates nothing; capturable into a HIP graph for a fixed n_rows.
+ * ref: engine/batched.cu:107-120 (decode_step_gpu), :44-72 (layer_forward_batched), :150
+ * (argmax_rows in model_decode_batch_greedy). */
 LLMK_API int llmk_engine_forward(llmk_engine* e, int n_rows, int n_logit_rows, int num_splits,
                                  void* stream);
 

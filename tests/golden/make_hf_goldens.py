@@ -8,15 +8,20 @@ reference checkout and the model weights are not available offline, so this scri
 same Hugging Face modules (transformers' LlamaRMSNorm, LlamaRotaryEmbedding +
 apply_rotary_pos_emb, the llama3 rope-init routine, SiLU, nn.Embedding) to seeded synthetic
 inputs of the reference's shapes. The vectors pin the oracle's rounding conventions
-independently of the oracle's own code. Run with the versions recorded in the file
-(transformers 5.15.0, torch 2.10.0).
+independently of the oracle's own code. It also runs LlamaForCausalLM in float32 over a prompt
+of a small Llama-3 shape with seeded random weights (tests/_helpers.py: TINY, tiny_weights), the
+whole-model anchor the reference takes from Hugging Face logits of the real model (ref:
+tests/test_generate_batched.cu:44-53); the fixture holds the token ids, the logits and a hash of
+the weights. Run with the versions recorded in the file (transformers 5.15.0, torch 2.10.0).
 
     python tests/golden/make_hf_goldens.py
 """
 from __future__ import annotations
 
+import hashlib
 import json
 import os
+import sys
 
 import numpy as np
 import torch
@@ -29,6 +34,40 @@ from transformers.models.llama.modeling_llama import (LlamaRMSNorm, LlamaRotaryE
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT = os.path.join(HERE, "hf_goldens.npz")
 SEED = 0x5EED0001
+# The whole-model case: tiny_weights(LLAMA_WEIGHT_SEED, embed_std=0.5), LLAMA_T token ids drawn
+# with default_rng(LLAMA_IDS_SEED).integers(0, vocab, LLAMA_T).
+LLAMA_WEIGHT_SEED, LLAMA_IDS_SEED, LLAMA_T = 0x5EED0110, 0x5EED0111, 40
+
+
+def weights_digest(w: dict) -> str:
+    """sha256 over the weights' names and fp16 bits in sorted-name order."""
+    h = hashlib.sha256()
+    for k in sorted(w):
+        h.update(k.encode())
+        h.update(np.ascontiguousarray(w[k]).view(np.uint16).tobytes())
+    return h.hexdigest()
+
+
+def tiny_llama_logits(c: dict, w: dict, ids) -> np.ndarray:
+    """Logits [T, vocab] of transformers' LlamaForCausalLM in float32 (eager attention, tied
+    embeddings, llama3 rope scaling) with the weights `w` (Hugging Face names), over one prompt."""
+    cfg = LlamaConfig(
+        vocab_size=c["vocab"], hidden_size=c["hidden"], intermediate_size=c["inter"],
+        num_hidden_layers=c["n_layers"], num_attention_heads=c["n_heads"],
+        num_key_value_heads=c["n_kv_heads"], head_dim=c["head_dim"],
+        max_position_embeddings=131072, rms_norm_eps=c["eps"], tie_word_embeddings=True,
+        rope_parameters={"rope_type": "llama3", "rope_theta": c["rope_theta"],
+                         "factor": c["rope_factor"], "low_freq_factor": c["rope_low_freq_factor"],
+                         "high_freq_factor": c["rope_high_freq_factor"],
+                         "original_max_position_embeddings": int(c["rope_original_max_pos"])},
+        attn_implementation="eager")
+    model = transformers.LlamaForCausalLM(cfg).float().eval()
+    state = {k: torch.from_numpy(v.astype(np.float32)) for k, v in w.items()}
+    state["lm_head.weight"] = state["model.embed_tokens.weight"]
+    missing, unexpected = model.load_state_dict(state, strict=False)
+    assert not unexpected and all("rotary" in m for m in missing), (missing, unexpected)
+    with torch.no_grad():
+        return model(torch.tensor(ids, dtype=torch.long)[None]).logits[0].numpy()
 
 
 def llama32_1b_config() -> LlamaConfig:
@@ -108,8 +147,19 @@ def main() -> None:
         e = emb(torch.from_numpy(ids).long())
     out.update(emb_table=table.view(np.uint16), emb_ids=ids, emb_out=e.numpy().view(np.uint16))
 
+    # Whole model: LlamaForCausalLM over a prompt, small Llama-3 shape, seeded random weights
+    sys.path.insert(0, os.path.dirname(HERE))
+    from _helpers import TINY, tiny_weights
+    w_tiny = tiny_weights(LLAMA_WEIGHT_SEED, embed_std=0.5)
+    llama_ids = np.random.default_rng(LLAMA_IDS_SEED).integers(0, TINY["vocab"], LLAMA_T)
+    out.update(llama_ids=llama_ids.astype(np.int32),
+               llama_logits=tiny_llama_logits(TINY, w_tiny, llama_ids).astype(np.float32))
+
     meta = {"seed": SEED, "transformers": transformers.__version__, "torch": torch.__version__,
-            "eps": cfg.rms_norm_eps, "rope": cfg.rope_parameters}
+            "eps": cfg.rms_norm_eps, "rope": cfg.rope_parameters,
+            "llama": {"config": TINY, "weight_seed": LLAMA_WEIGHT_SEED, "embed_std": 0.5,
+                      "ids_seed": LLAMA_IDS_SEED, "T": LLAMA_T,
+                      "weights_sha256": weights_digest(w_tiny)}}
     out["meta_json"] = np.frombuffer(json.dumps(meta).encode(), dtype=np.uint8)
     np.savez_compressed(OUT, **out)
     print(f"wrote {OUT}: " + ", ".join(f"{k}{list(v.shape)}" for k, v in out.items()))

@@ -73,27 +73,25 @@ def test_linear_matches_torch_float32_linear():
 # ------------------------------------------------------------------------------------------
 # engine_forward
 # ------------------------------------------------------------------------------------------
-def _hf_logits(w, ids):
-    torch = pytest.importorskip("torch")
-    transformers = pytest.importorskip("transformers")
-    c = TINY
-    cfg = transformers.LlamaConfig(
-        vocab_size=c["vocab"], hidden_size=c["hidden"], intermediate_size=c["inter"],
-        num_hidden_layers=c["n_layers"], num_attention_heads=c["n_heads"],
-        num_key_value_heads=c["n_kv_heads"], head_dim=c["head_dim"],
-        max_position_embeddings=131072, rms_norm_eps=c["eps"], tie_word_embeddings=True,
-        rope_parameters={"rope_type": "llama3", "rope_theta": c["rope_theta"],
-                         "factor": c["rope_factor"], "low_freq_factor": c["rope_low_freq_factor"],
-                         "high_freq_factor": c["rope_high_freq_factor"],
-                         "original_max_position_embeddings": int(c["rope_original_max_pos"])},
-        attn_implementation="eager")
-    model = transformers.LlamaForCausalLM(cfg).float().eval()
-    state = {k: torch.from_numpy(v.astype(np.float32)) for k, v in w.items()}
-    state["lm_head.weight"] = state["model.embed_tokens.weight"]
-    missing, unexpected = model.load_state_dict(state, strict=False)
-    assert not unexpected and all("rotary" in m for m in missing), (missing, unexpected)
-    with torch.no_grad():
-        return model(torch.tensor(ids, dtype=torch.long)[None]).logits[0].numpy()
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hf_goldens.npz")
+
+
+def _hf_case():
+    """The whole-model Hugging Face case of tests/golden/hf_goldens.npz: the seeded weights
+    (regenerated here and checked against the hash the fixture records), the prompt's token ids
+    and LlamaForCausalLM's float32 logits over it."""
+    import hashlib
+    import json
+    g = np.load(GOLDEN)
+    meta = json.loads(bytes(g["meta_json"]).decode())["llama"]
+    assert meta["config"] == TINY
+    w = _tiny_weights(meta["weight_seed"], embed_std=meta["embed_std"])
+    h = hashlib.sha256()
+    for k in sorted(w):
+        h.update(k.encode())
+        h.update(np.ascontiguousarray(w[k]).view(np.uint16).tobytes())
+    assert h.hexdigest() == meta["weights_sha256"], "tiny_weights no longer gives the fixture's"
+    return w, g["llama_ids"].astype(np.int64), g["llama_logits"].astype(np.float64)
 
 
 def _prompt_rows(ids, pages, max_pages, start=0):
@@ -105,20 +103,19 @@ def _prompt_rows(ids, pages, max_pages, start=0):
 
 def test_engine_forward_matches_hugging_face_llama():
     """The oracle's forward pass over a prompt (one row per token, all with the sequence's
-    shuffled block table) against LlamaForCausalLM in float32 on the same weights: logits of
+    shuffled block table) against LlamaForCausalLM in float32 on the same weights (the committed
+    fixture tests/golden/hf_goldens.npz, made by tests/golden/make_hf_goldens.py): logits of
     every position within a relative L2 of 5e-3 (the reference's bar for its fp16 engine
     against Hugging Face; measured 1.0e-3), and the same greedy token wherever Hugging Face's
     top two differ by more than 0.05."""
-    w = _tiny_weights(0x5EED0110, embed_std=0.5)
-    rng = np.random.default_rng(0x5EED0111)
-    T, max_pages, num_pages = 40, 8, 16
-    ids = rng.integers(0, TINY["vocab"], T)
+    w, ids, ref = _hf_case()
+    rng = np.random.default_rng(0x5EED0112)
+    T, max_pages, num_pages = len(ids), 8, 16
     pages = rng.permutation(num_pages)[:max_pages].astype(np.int32)
     tok, pos, tab = _prompt_rows(ids, pages, max_pages)
     kp, vp = _pools(num_pages)
     logits, nxt, _ = oracle.engine_forward(TINY, w, tok, pos, tab, kp, vp)
     got = logits.view(np.float16).astype(np.float64)
-    ref = _hf_logits(w, ids).astype(np.float64)
     rel = np.linalg.norm(got - ref, axis=1) / np.linalg.norm(ref, axis=1)
     assert rel.max() < 5e-3, rel.max()
     top2 = np.sort(ref, axis=1)[:, -2:]

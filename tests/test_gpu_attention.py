@@ -5,7 +5,9 @@ its sequence lengths (page-boundary cases 15/16/17, one position, 2048), its spl
 pre-filled with NaN patterns, and its pass rule |d| <= 1e-3 + 4e-3 |e| for every element.
 
 The kernel sums in another order than the oracle (which follows the reference's plain paged
-kernel), so the bar is the reference's tolerance, plus a floor on the bit-identical share."""
+kernel), so the bar is the reference's tolerance, plus a floor on the bit-identical share: at
+least 99% of the output elements equal the oracle's bit for bit (a drift of a systematic kind
+on a few percent of the elements fails it)."""
 import numpy as np
 import pytest
 import torch
@@ -14,6 +16,7 @@ from _helpers import ATTN_LENS, POISON, assert_tol, attention_case
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
+EXACT_FLOOR = 0.99  # share of bit-identical output elements
 
 
 def dev(bits: np.ndarray) -> torch.Tensor:
@@ -73,14 +76,14 @@ def test_reference_lengths_and_splits(llmk, orc, reference_case, splits):
     got = d.run(llmk, splits)
     cmp = orc.compare(got, oracle_out(orc, reference_case))
     print(f"splits {splits}: max_abs {cmp['max_abs']:.2e} exact {100 * cmp['exact']:.2f}%")
-    assert_tol(cmp, 0.75, f"attention splits={splits}")
+    assert_tol(cmp, EXACT_FLOOR, f"attention splits={splits}")
 
 
 def test_results_do_not_depend_much_on_the_split_count(llmk, orc, reference_case):
     d = OnDevice(reference_case)
     one = d.run(llmk, 1)
     for splits in (2, 5, 32):
-        assert_tol(orc.compare(d.run(llmk, splits), one), 0.75, f"splits {splits} vs 1")
+        assert_tol(orc.compare(d.run(llmk, splits), one), EXACT_FLOOR, f"splits {splits} vs 1")
 
 
 @pytest.mark.parametrize("nkv", [1, 2, 4, 16])
@@ -92,7 +95,7 @@ def test_other_kv_head_counts(llmk, orc, nkv):
     d = OnDevice(c)
     for splits in (1, 3):
         cmp = orc.compare(d.run(llmk, splits), oracle_out(orc, c))
-        assert_tol(cmp, 0.75, f"n_kv {nkv} splits {splits}")
+        assert_tol(cmp, EXACT_FLOOR, f"n_kv {nkv} splits {splits}")
 
 
 @pytest.mark.parametrize("splits", [32, 43, 64, 128])
@@ -102,7 +105,7 @@ def test_small_batch_in_short_runs(llmk, orc, reference_case, splits):
     sequence, four rounds of the merge)."""
     d = OnDevice(reference_case)
     cmp = orc.compare(d.run(llmk, splits), oracle_out(orc, reference_case))
-    assert_tol(cmp, 0.75, f"short runs, splits {splits}")
+    assert_tol(cmp, EXACT_FLOOR, f"short runs, splits {splits}")
 
 
 @pytest.mark.parametrize("nkv", [1, 2, 4, 16])
@@ -115,7 +118,7 @@ def test_short_runs_with_other_kv_head_counts(llmk, orc, nkv):
     d = OnDevice(c)
     ref = oracle_out(orc, c)
     for splits in (8, 16, 32):
-        assert_tol(orc.compare(d.run(llmk, splits), ref), 0.75, f"n_kv {nkv} splits {splits}")
+        assert_tol(orc.compare(d.run(llmk, splits), ref), EXACT_FLOOR, f"n_kv {nkv} splits {splits}")
 
 
 def test_empty_sequences_give_nan_and_leave_the_rest_intact(llmk, orc):
@@ -126,7 +129,7 @@ def test_empty_sequences_give_nan_and_leave_the_rest_intact(llmk, orc):
         got = d.run(llmk, splits, fill=0x1234).reshape(4, -1)
         for b in (0, 2):
             assert np.all(np.isnan(got[b].view(np.float16))), f"seq {b} splits {splits}"
-        assert_tol(orc.compare(got[[1, 3]].reshape(-1), ref[[1, 3]].reshape(-1)), 0.75,
+        assert_tol(orc.compare(got[[1, 3]].reshape(-1), ref[[1, 3]].reshape(-1)), EXACT_FLOOR,
                    "non-empty rows")
 
 
@@ -142,7 +145,7 @@ def test_single_position_returns_the_value_row_exactly(llmk, orc):
 def test_workspace_may_be_null_with_one_split(llmk, orc, reference_case):
     d = OnDevice(reference_case)
     got = d.run(llmk, 1, workspace=None)
-    assert_tol(orc.compare(got, oracle_out(orc, reference_case)), 0.75, "no workspace")
+    assert_tol(orc.compare(got, oracle_out(orc, reference_case)), EXACT_FLOOR, "no workspace")
 
 
 def test_preconditions_are_reported(llmk, reference_case):
@@ -185,7 +188,7 @@ def test_on_a_side_stream(llmk, orc, reference_case):
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         got = d.run(llmk, 4, stream=s)
-    assert_tol(orc.compare(got, oracle_out(orc, reference_case)), 0.75, "side stream")
+    assert_tol(orc.compare(got, oracle_out(orc, reference_case)), EXACT_FLOOR, "side stream")
 
 
 def test_decode_batch_of_256_sequences_up_to_2048(llmk, orc):
@@ -198,7 +201,7 @@ def test_decode_batch_of_256_sequences_up_to_2048(llmk, orc):
     ref = oracle_out(orc, c)
     for splits in (llmk.choose_num_splits(256, 8, int(lens.max())),
                    llmk.choose_num_splits(256, 8, int(lens.max()), 64)):
-        assert_tol(orc.compare(d.run(llmk, splits), ref), 0.75, f"batch 256 splits {splits}")
+        assert_tol(orc.compare(d.run(llmk, splits), ref), EXACT_FLOOR, f"batch 256 splits {splits}")
 
 
 def test_many_short_sequences_share_a_block(llmk, orc):
@@ -209,7 +212,7 @@ def test_many_short_sequences_share_a_block(llmk, orc):
     d = OnDevice(c)
     ref = oracle_out(orc, c)
     for splits in (3, 8, 32):
-        assert_tol(orc.compare(d.run(llmk, splits), ref), 0.75, f"short seqs splits {splits}")
+        assert_tol(orc.compare(d.run(llmk, splits), ref), EXACT_FLOOR, f"short seqs splits {splits}")
     c1 = attention_case(rng, rng.integers(0, 17, 64))
     assert c1["max_pages"] == 1
     d1 = OnDevice(c1)
@@ -218,5 +221,5 @@ def test_many_short_sequences_share_a_block(llmk, orc):
     for splits in (1, 8):
         got = d1.run(llmk, splits).reshape(64, -1)
         assert np.all(np.isnan(got[empty].view(np.float16)))
-        assert_tol(orc.compare(got[~empty].reshape(-1), ref1[~empty].reshape(-1)), 0.75,
+        assert_tol(orc.compare(got[~empty].reshape(-1), ref1[~empty].reshape(-1)), EXACT_FLOOR,
                    f"one-page sequences splits {splits}")

@@ -485,7 +485,10 @@ def test_engine_graph_replays_match_eager(llmk, orc):
     pages = rng.permutation(64).astype(np.int32).reshape(16, 4)
     tab = np.array([pages[0]] * 5 + [pages[1]] * 7, np.int32)
     e.set_rows(tok, pos, tab)
-    e.forward(n)                      # eager: chooses the GEMM plans before capture
+    # A pass captured with num_splits = 0 takes the capacity rule (the rows' short contexts
+    # would give one split): the eager reference uses that count explicitly.
+    splits = min(65536 // (n * TINY["n_kv_heads"]), 4, 32)
+    e.forward(n, num_splits=splits)   # eager: chooses the GEMM plans before capture
     torch.cuda.synchronize()
     ref_logits = e.logits(n).view(torch.int16).clone()
     ref_pool = e.pool(llmk.BUF_K_POOL, 1).view(torch.int16).clone()
@@ -549,6 +552,34 @@ def test_engine_rejects_rows_that_address_outside_its_buffers(llmk):
         e.set_rows(**ok, logit_rows=[2])
     with pytest.raises(llmk.LlmkError):
         e.forward(5)                                   # more rows than max_rows
+
+
+def test_engine_rejects_a_pass_over_rows_not_uploaded(llmk):
+    """A pass may not ask for more rows (or logit rows) than the last set_rows uploaded: the
+    device copies past them were never checked. The call fails before any launch, so the
+    outputs of the previous pass stay as they were."""
+    e = make_engine(llmk, TINY, tiny_weights(0x5EED0270, embed_std=0.5), 4, 2, 8)
+    s = torch.cuda.Stream()
+    with pytest.raises(llmk.LlmkError) as ei:
+        e.forward(1)                                   # nothing uploaded yet
+    assert ei.value.status == llmk.LLMK_ERR_INVALID_VALUE
+    e.set_rows([1, 2, 3], [0, 5, 17], [[0, 1], [2, 3], [4, 5]], logit_rows=[2])
+    e.forward(3, 1)
+    torch.cuda.synchronize()
+    before = e.logits(1).view(torch.int16).clone()
+    e.set_rows([4, 5], [1, 2], [[0, 1], [2, 3]])
+    for n, nl in ((3, -1), (2, 1), (3, 1)):
+        with pytest.raises(llmk.LlmkError) as ei:
+            e.forward(n, nl)
+        assert ei.value.status == llmk.LLMK_ERR_INVALID_VALUE
+        with pytest.raises(llmk.LlmkError) as ei:
+            e.forward_graph(n, nl, stream=s)
+        assert ei.value.status == llmk.LLMK_ERR_INVALID_VALUE
+    torch.cuda.synchronize()
+    assert torch.equal(e.logits(1).view(torch.int16), before)
+    e.forward(2)                                       # the rows that were uploaded
+    torch.cuda.synchronize()
+    assert not torch.isnan(e.logits(2).float()).any()
     with pytest.raises(llmk.LlmkError) as ei:
         llmk.Engine(llmk.ModelConfig(**dict(TINY, head_dim=128)), 4, 2, 8)
     assert ei.value.status == llmk.LLMK_ERR_SHAPE
