@@ -5,8 +5,12 @@ Headline (the JSON line's `value`): the fused residual add + RMSNorm over [8192,
 -- whole-job throughput in GB/s of algorithmic bytes (inputs read once,
 outputs written once), inputs resident in HBM before the timed region. One step = one launch
 over the full batch. The other BASELINE configurations (RMSNorm [16,2048], RoPE, SwiGLU,
-embedding gather, the 16-layer decode-step pass captured in a HIP graph) and a copy probe are
-measured the same way and reported under "kernels".
+embedding gather, the 16-layer decode-step pass captured in HIP graphs) are measured the same
+way and reported under "kernels", each with the scalar CPU oracle of the same work timed on the
+host's cores in the same run ("cpu") and the bandwidth ceiling of its traffic mix ("ceiling").
+The pass is also broken down by stage: one HIP graph per op type (16 launches each) and a graph
+of empty kernels in the pass's 49 launch shapes, its launch floor (ref:
+bench/bench_breakdown.cu:18-26,58-104 times each stage of a layer with its own events).
 
 Caches: MI355X has a 256 MB Infinity Cache (MALL) in front of HBM and 4 MB of L2 per XCD. Each
 kernel cycles through enough independent input sets that the data of a launch was last
@@ -18,14 +22,23 @@ short spin kernel with a HIP event right before the first and right after the la
 the stream they are launched on (torch's current stream); the mean launch duration is the event
 interval / K, and `roofline.achieved` = algorithmic bytes / that mean.
 
+Ceilings (ref: bench/bandwidth.cu:11-62, a copy kernel swept over block and grid sizes): the
+bandwidth probes of llmk_bw_probe -- read-only, 1:1 copy, 2:1 read:write, in-place rewrite,
+write-only -- swept over grid and unroll at 1 GiB, and run again at each kernel's own byte
+count and traffic mix.
+
+Profiles: every measurement is preceded by a marker launch (an empty kernel whose grid names the
+section, SECTIONS below), so `--summarize-profiles` can group a rocprofv3 trace by section.
+
 CPU baseline: the scalar C oracle of the same op (oracle/, test infrastructure) on the host's
 cores, over a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--kernels all|headline] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--kernels all|headline|...] [--no-cpu]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -35,8 +48,25 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = ("achieved HBM GB/s (% of ~8 TB/s) per fused kernel; "
           "µs per 16-layer non-GEMM pass")
 PEAK_GBS = 8000.0
-WARM_S = 0.25
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "llmk_kernels_bench_configs.txt")
+
+# Marker launches: llmk_empty_launch(MARK_BASE + index, 64) before each measurement.
+MARK_BASE = 50000
+SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_8192",
+            "pass_graph", "pass_eager", "pass_floor", "pass_stage_embedding",
+            "pass_stage_add_rmsnorm", "pass_stage_rope_kv_scatter", "pass_stage_swiglu",
+            "pass_floor_stages", "attention_256", "attention_16x2048", "attention_sweep",
+            "argmax", "step_256", "step_8", "sched", "probe_sweep", "probe_kernels", "copy_1GiB",
+            "end"]
+
+# Launch shapes (blocks, threads) of the 16-layer pass at 256 sequences, from the launchers'
+# grid rules: the embedding and add+RMSNorm take one 64-thread wave per row below 4096 rows
+# (gather_scatter.hip rows_grid, norm.hip rmsnorm_launch); the fused RoPE + scatter one token
+# per 256-thread block below 2048 tokens (rope.hip tokens_per_block: 48 vectors of 16 B per
+# token, 2 per thread); SwiGLU 512 vectors per 256-thread block (swiglu.hip, UNROLL 2) over
+# 256 x 8192 values.
+PASS_SHAPES = {"embedding": (256, 64), "add_rmsnorm": (256, 64),
+               "rope_kv_scatter": (256, 256), "swiglu": (512, 256)}
 
 
 def log(msg: str) -> None:
@@ -48,13 +78,20 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--kernels", choices=["all", "headline", "step", "step8", "sched"],
-                    default="all",
-                    help="all: every configuration; headline: config 2 only; step / step8: "
-                         "config 2 and the engine's decode step of 256 / 8 sequences; sched: "
-                         "config 2 and the reference's scheduler workload")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--kernels", default="all",
+                    choices=["all", "kernels", "headline", "configs", "pass", "attn", "probe",
+                             "step", "step8", "sched"],
+                    help="all: everything; kernels: all but the engine step and the scheduler "
+                         "(for counter runs); headline: config 2 only; configs: configs 1-4, the "
+                         "pass and the probes; pass: the decode pass and its breakdown; attn: decode "
+                         "attention and its batch sweep; probe: bandwidth probes; step / step8: "
+                         "the engine's decode step of 256 / 8 sequences; sched: the reference's "
+                         "scheduler workload (config 2 is always measured)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0,
+                    help="CPU time per configuration (all cores 70%%, one core 30%%)")
+    ap.add_argument("--warm-seconds", type=float, default=0.25,
+                    help="minimum back-to-back warm-up per measurement")
     ap.add_argument("--summarize-profiles", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
                     help="summarise rocprofv3 csv output of this bench instead of running it")
     ap.add_argument("--summarize-sched", metavar="TRACE_DIR",
@@ -79,145 +116,176 @@ def read_traffic() -> dict:
     return out
 
 
-
-# (label, kernel-name substring, grid size in work-items, algorithmic bytes) of each measured
-# launch shape; grid sizes follow from the launchers' grid choices at the benchmark shapes.
+# ---------------------------------------------------------------------------------------------
+# rocprofv3 summaries
+# ---------------------------------------------------------------------------------------------
 # Decode attention over 256 sequences with lengths uniform in [1, 2048] (seed 0x5EED0006):
 # the bytes of bytes_attention(attention_lens()) in cuda-llm-engine_amd/workloads.py.
 ATTN_BYTES_256 = 546_019_628
 ATTN_BYTES_16x2048 = 67_248_192  # 16 sequences x 2048 positions
 
+# (label, section, kernel-name substring, grid size in work-items, algorithmic bytes) of each
+# measured launch shape whose counters are reported; grid sizes follow from the launchers'
+# grid choices at the benchmark shapes.
 PROFILE_SHAPES = [
-    ("add_rmsnorm_8192x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 8192 * 64, 134221824),
-    ("rmsnorm_16x2048", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
+    ("add_rmsnorm_8192x2048", "headline", "k_rmsnorm_waveILi4ELb1ELb1E", 8192 * 64, 134221824),
+    ("rmsnorm_16x2048", "rmsnorm_16", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
     # 8 tokens per block, 10 vector tasks per thread (40 heads x 8 vectors x 8 tokens / 256)
-    ("rope_8192", "k_rope_vecILi4ELi10ELb0E", 1024 * 256, 83918976),
-    ("swiglu_8192x8192", "k_swiglu_vecILi2E", 16384 * 256, 402653184),
-    ("embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
-    ("copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),
+    ("rope_8192", "rope_8192", "k_rope_vec", 1024 * 256, 83918976),
+    ("swiglu_8192x8192", "swiglu_8192", "k_swiglu_vecILi2E", 16384 * 256, 402653184),
+    ("embedding_8192", "embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
+    ("copy_1GiB", "copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),
     # 512 blocks: two resident blocks of 256 threads on each of the 256 CUs (191 VGPRs).
-    ("attention_decode_256", "k_attn_balancedILi8E", 512 * 256, ATTN_BYTES_256,
-     ("k_attn_merge", 256 * 256)),
+    ("attention_decode_256", "attention_256", "k_attn_balancedILi8E", 512 * 256,
+     ATTN_BYTES_256),
+    ("attention_merge_256", "attention_256", "k_attn_merge", 256 * 256, None),
     # 16 sequences take the sequence-split grid (32 splits of 4 pages, 16 blocks per split).
-    ("attention_decode_16x2048", "k_attn_splitILi8ELi0E", 32 * 256 * 16, ATTN_BYTES_16x2048,
-     ("k_attn_merge_many", 8 * 256 * 16)),
-    ("argmax_256x128256", "k_argmax_vec", 256 * 1024, 256 * 128256 * 2 + 256 * 4),
-    ("decode:embedding_256", "k_embeddingILi0E", 256 * 64, 2098176),
-    ("decode:add_rmsnorm_256x2048", "k_rmsnorm_waveILi4ELb1ELb1E", 256 * 64, 4198400),
-    ("decode:rope_kv_scatter_256", "k_rope_vecILi4ELi2ELb1E", 256 * 256, 3147904),
-    ("decode:swiglu_256x8192", "k_swiglu_vecILi2E", 512 * 256, 12582912),
+    ("attention_decode_16x2048", "attention_16x2048", "k_attn_splitILi8ELi0E", 32 * 256 * 16,
+     ATTN_BYTES_16x2048),
+    ("attention_merge_16x2048", "attention_16x2048", "k_attn_merge_many", 8 * 256 * 16, None),
+    ("argmax_256x128256", "argmax", "k_argmax_vec", 256 * 1024, 256 * 128256 * 2 + 256 * 4),
+    ("decode:embedding_256", "pass_graph", "k_embeddingILi0E", 256 * 64, 2098176),
+    ("decode:add_rmsnorm_256x2048", "pass_graph", "k_rmsnorm_waveILi4ELb1ELb1E", 256 * 64,
+     4198400),
+    ("decode:rope_kv_scatter_256", "pass_graph", "k_rope_vecILi4ELi2ELb1ELb0E", 256 * 256,
+     3147904),
+    ("decode:swiglu_256x8192", "pass_graph", "k_swiglu_vecILi2E", 512 * 256, 12582912),
 ]
 
 
-def summarize_profiles(trace_dir, fetch_dir, write_dir):
-    """Per launch shape: mean kernel duration from the kernel trace, FETCH_SIZE and WRITE_SIZE per
-    dispatch, and HBM traffic per launch with each counter scaled by what it reads for the
-    1 GiB copy probe (1 GiB read, 1 GiB written)."""
+def _grid(r) -> int:
+    if "Grid_Size_X" in r:
+        return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+    return int(r["Grid_Size"])
+
+
+def _csv_rows(d, suffix):
     import csv
     import glob
+    out = []
+    for f in glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True):
+        out += list(csv.DictReader(open(f)))
+    return out
 
-    def rows(d, suffix):
-        out = []
-        for f in glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True):
-            out += list(csv.DictReader(open(f)))
-        return out
 
-    def grid(r):
-        if "Grid_Size_X" in r:
-            return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
-        return int(r["Grid_Size"])
+def _by_section(table):
+    """Rows in dispatch order, each tagged with the section of the last marker before it;
+    marker dispatches themselves are dropped."""
+    table = sorted(table, key=lambda r: int(r["Dispatch_Id"]))
+    cur, out = None, []
+    for r in table:
+        g = _grid(r)
+        if "k_empty" in r["Kernel_Name"] and g % 64 == 0 and g // 64 >= MARK_BASE:
+            i = g // 64 - MARK_BASE
+            cur = SECTIONS[i] if i < len(SECTIONS) else None
+            continue
+        out.append((cur, r))
+    return out
 
-    def matches(table):
-        """(label, row) for every row of a launch shape; a shape with a 5th field also needs
-        the next dispatch to be that (kernel, grid) -- the attention kernel is told apart by
-        the merge launch that follows it."""
-        by_id = {int(r["Dispatch_Id"]): r for r in table}
-        for r in table:
-            for shape in PROFILE_SHAPES:
-                label, name, g = shape[:3]
-                if name not in r["Kernel_Name"] or grid(r) != g:
-                    continue
-                if len(shape) > 4:
-                    nxt = by_id.get(int(r["Dispatch_Id"]) + 1)
-                    if nxt is None or shape[4][0] not in nxt["Kernel_Name"] \
-                            or grid(nxt) != shape[4][1]:
-                        continue
-                yield label, r
 
-    dur, cnt = {}, {}
-    for label, r in matches(rows(trace_dir, "kernel_trace.csv")):
-        dur.setdefault(label, []).append(
+def summarize_profiles(trace_dir, fetch_dir, write_dir):
+    """Per section of the run: every (kernel, grid) with its mean, min and max duration from the
+    kernel trace; FETCH_SIZE and WRITE_SIZE per dispatch; and for the launch shapes of
+    PROFILE_SHAPES the HBM traffic per launch, each counter scaled by what it reads for the
+    1 GiB copy probe (1 GiB read, 1 GiB written). For the decode pass: kernel time per pass."""
+    dur = {}
+    for sec, r in _by_section(_csv_rows(trace_dir, "kernel_trace.csv")):
+        key = (sec, r["Kernel_Name"], _grid(r))
+        dur.setdefault(key, []).append(
             (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+    cnt = {}
     for d, cname in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
-        table = [r for r in rows(d, "counter_collection.csv") if r["Counter_Name"] == cname]
-        for label, r in matches(table):
-            cnt.setdefault((label, cname), []).append(float(r["Counter_Value"]))
+        table = [r for r in _csv_rows(d, "counter_collection.csv") if r["Counter_Name"] == cname]
+        for sec, r in _by_section(table):
+            cnt.setdefault((sec, r["Kernel_Name"], _grid(r), cname), []).append(
+                float(r["Counter_Value"]))
     avg = {k: sum(v) / len(v) for k, v in cnt.items() if v}
+
+    def find(section, name, grid):
+        keys = [k for k in dur if k[0] == section and name in k[1] and k[2] == grid]
+        return keys[0] if keys else None
+
     print("# rocprofv3 summaries of bench.py on one MI355X (gfx950), made by:")
     print(f"#   rocprofv3 --kernel-trace --stats -f csv -d {trace_dir} -o bench -- "
           "python3 bench.py --no-cpu")
     print(f"#   rocprofv3 --pmc FETCH_SIZE -f csv -d {fetch_dir} -o fetch -- "
-          "python3 bench.py --no-cpu --steps 20 --warmup 2")
+          "python3 bench.py --no-cpu --kernels kernels --steps 20 --warmup 2 --warm-seconds 0")
     print(f"#   rocprofv3 --pmc WRITE_SIZE -f csv -d {write_dir} -o write -- "
-          "python3 bench.py --no-cpu --steps 20 --warmup 2")
+          "python3 bench.py --no-cpu --kernels kernels --steps 20 --warmup 2 --warm-seconds 0")
     print(f"#   python3 bench.py --summarize-profiles {trace_dir} {fetch_dir} {write_dir}")
     print("#")
-    print("# rocprofv3 --stats, libllmk kernels (all launch shapes of the run together):")
-    print("#   calls  avg_us  min_us  max_us  kernel")
-    for r in rows(trace_dir, "kernel_stats.csv"):
-        if "llmk" in r["Name"]:
-            print(f"#   {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:8.3f} "
-                  f"{float(r['MinNs']) / 1e3:8.3f} {float(r['MaxNs']) / 1e3:8.3f}  {r['Name'][:90]}")
-    print("#")
+    ck = find("copy_1GiB", "k_copy", 8192 * 256)
+    if ck is None or (ck + ("FETCH_SIZE",)) not in avg or (ck + ("WRITE_SIZE",)) not in avg:
+        print("copy_1GiB MISSING (kernel name or grid not found)")
+        return 1
     copy_b = 1 << 30
-    sf = copy_b / (avg[("copy_1GiB", "FETCH_SIZE")] * 1024)
-    sw = copy_b / (avg[("copy_1GiB", "WRITE_SIZE")] * 1024)
-    print(f"# Per launch shape. us_mean: mean kernel duration in the kernel trace. fetch_kib and")
-    print(f"# write_kib: FETCH_SIZE and WRITE_SIZE per dispatch. traffic_bytes = fetch_kib*1024*"
-          f"{sf:.4f} + write_kib*1024*{sw:.4f}, the factors being 1 GiB over what each counter")
-    print("# reads for the 1 GiB copy probe (1 GiB read and 1 GiB written per launch).")
+    sf = copy_b / (avg[ck + ("FETCH_SIZE",)] * 1024)
+    sw = copy_b / (avg[ck + ("WRITE_SIZE",)] * 1024)
+    print("# Launch shapes. us_mean: mean kernel duration in the kernel trace (all launches of the")
+    print("# shape in its section). fetch_kib, write_kib: FETCH_SIZE and WRITE_SIZE per dispatch.")
+    print(f"# traffic_bytes = fetch_kib*1024*{sf:.4f} + write_kib*1024*{sw:.4f}, the factors being")
+    print("# 1 GiB over what each counter reads for the 1 GiB copy probe (1 GiB read and 1 GiB")
+    print("# written per launch).")
     missing = []
-    for label, _, _, alg, *_ in PROFILE_SHAPES:
-        d = dur.get(label, [])
-        f, w = avg.get((label, "FETCH_SIZE")), avg.get((label, "WRITE_SIZE"))
-        us = f"{sum(d) / len(d):.3f}" if d else "-"
-        if f is None or w is None or not d:
-            print(f"{label} us_mean={us} calls={len(d)} MISSING (kernel name or grid not found)")
+    for label, sec, name, g, alg in PROFILE_SHAPES:
+        k = find(sec, name, g)
+        if k is None:
+            print(f"{label} MISSING (kernel name or grid not found in section {sec})")
             missing.append(label)
             continue
-        traffic = f * 1024 * sf + w * 1024 * sw
-        print(f"{label} us_mean={us} calls={len(d)} fetch_kib={f:.1f} write_kib={w:.1f} "
-              f"traffic_bytes={traffic:.0f} algorithmic_bytes={alg} ratio={traffic / alg:.4f}")
+        d = dur[k]
+        f, w = avg.get(k + ("FETCH_SIZE",)), avg.get(k + ("WRITE_SIZE",))
+        line = (f"{label} us_mean={sum(d) / len(d):.3f} us_min={min(d):.3f} "
+                f"us_max={max(d):.3f} calls={len(d)}")
+        if f is not None and w is not None:
+            traffic = f * 1024 * sf + w * 1024 * sw
+            line += f" fetch_kib={f:.1f} write_kib={w:.1f} traffic_bytes={traffic:.0f}"
+            if alg:
+                line += f" algorithmic_bytes={alg} ratio={traffic / alg:.4f}"
+        print(line)
+    print("#")
+    print("# Every kernel of every section: calls, mean / min / max duration (us), grid")
+    print("# (work-items), kernel.")
+    sections = []
+    for k in dur:
+        if k[0] not in sections:
+            sections.append(k[0])
+    for sec in sections:
+        print(f"## section {sec}")
+        for k in sorted((k for k in dur if k[0] == sec), key=lambda k: -sum(dur[k])):
+            d = dur[k]
+            print(f"#   {len(d):6d} {sum(d) / len(d):9.3f} {min(d):9.3f} {max(d):9.3f} "
+                  f"{k[2]:9d}  {k[1][:96]}")
+    # kernel time per pass: the pass graph's kernels over its number of passes (embeddings)
+    pk = [k for k in dur if k[0] == "pass_graph"]
+    passes = sum(len(dur[k]) for k in pk if "k_embedding" in k[1])
+    if passes:
+        total = sum(sum(dur[k]) for k in pk) / passes
+        print("#")
+        print(f"# pass_graph: {passes} passes, kernel time per pass {total:.2f} us "
+              f"(sum of the 49 kernels' durations; the event-timed pass includes the gaps)")
+        for k in sorted(pk, key=lambda k: -sum(dur[k])):
+            print(f"#   {len(dur[k]) / passes:6.2f} launches/pass x {sum(dur[k]) / len(dur[k]):7.3f}"
+                  f" us = {sum(dur[k]) / passes:7.2f} us/pass  {k[1][:80]}")
     return 1 if missing else 0
 
 
 def summarize_step(trace_dir, n_rows=256):
-    """Kernels of the engine's decode step (the dispatches between the first and the last
-    embedding gather of n_rows rows, i.e. the graph replays), grouped by kernel name and grid
-    size: launches per step, mean duration, and time per step."""
-    import csv
-    import glob
-    rows = []
-    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
-        rows += list(csv.DictReader(open(f)))
-    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-
-    def grid(r):
-        return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
-
-    starts = [i for i, r in enumerate(rows) if "k_embedding" in r["Kernel_Name"]
-              and grid(r) == n_rows * 64]
-    if len(starts) < 3:
-        print("no decode steps found")
+    """Kernels of the engine's decode step (the graph replays of the bench's step_256 or step_8
+    section), grouped by kernel name and grid size: launches per step, mean duration, and time
+    per step."""
+    sec = "step_256" if n_rows == 256 else "step_8"
+    rows = [r for s_, r in _by_section(_csv_rows(trace_dir, "kernel_trace.csv")) if s_ == sec]
+    # only the step's own kernels (libllmk and hipBLASLt), not the bench's spin kernels
+    steps = [r for r in rows if "llmk" in r["Kernel_Name"] or r["Kernel_Name"].startswith("Cijk")]
+    n_steps = sum(1 for r in steps if "k_embedding" in r["Kernel_Name"]
+                  and _grid(r) == n_rows * 64)
+    if n_steps == 0:
+        print(f"no decode steps found in section {sec}")
         return
-    # whole steps, skipping the eager first pass; only the step's own kernels (libllmk and
-    # hipBLASLt), not the bench's spin or fill kernels in between
-    steps = [r for r in rows[starts[1]:starts[-1]]
-             if "llmk" in r["Kernel_Name"] or r["Kernel_Name"].startswith("Cijk")]
-    n_steps = len(starts) - 2
     agg = {}
     for r in steps:
-        key = (r["Kernel_Name"], grid(r))
+        key = (r["Kernel_Name"], _grid(r))
         agg.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     print(f"# engine decode step (Llama-3.2-1B shape, {n_rows} rows), {n_steps} graph replays")
     print("# launches/step  mean_us  us/step  grid  kernel")
@@ -234,16 +302,8 @@ def summarize_sched(trace_dir, min_passes=20, top=10):
     embedding gather to the next argmax (a gather of logit rows inside the pass is part of it).
     For every row count with at least min_passes passes: passes, kernel time per pass, and the
     top kernels (launches per pass, mean duration, time per pass, grid)."""
-    import csv
-    import glob
-    rows = []
-    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
-        rows += list(csv.DictReader(open(f)))
-    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-
-    def grid(r):
-        return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
-
+    rows = [r for s_, r in _by_section(_csv_rows(trace_dir, "kernel_trace.csv"))
+            if s_ == "sched"]
     passes, cur = {}, None
     for r in rows:
         name = r["Kernel_Name"]
@@ -252,8 +312,8 @@ def summarize_sched(trace_dir, min_passes=20, top=10):
         if cur is None:
             if "k_embedding" not in name:
                 continue
-            cur = {"n": grid(r) // 64, "k": []}
-        cur["k"].append((name, grid(r), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+            cur = {"n": _grid(r) // 64, "k": []}
+        cur["k"].append((name, _grid(r), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
         if "k_argmax" in name:
             passes.setdefault(cur["n"], []).append(cur["k"])
             cur = None
@@ -274,6 +334,9 @@ def summarize_sched(trace_dir, min_passes=20, top=10):
                   f"{g:9d}  {name[:100]}")
 
 
+# ---------------------------------------------------------------------------------------------
+# timing
+# ---------------------------------------------------------------------------------------------
 class Timer:
     """Two timed passes of `steps` launches each.
 
@@ -285,8 +348,9 @@ class Timer:
        launch duration is the event interval / steps: the launches run back to back on the GPU.
     """
 
-    def __init__(self, torch):
+    def __init__(self, torch, warm_s: float):
         self.torch = torch
+        self.warm_s = warm_s
         self.cycles_per_s = None
 
     def _calibrate(self):
@@ -300,16 +364,17 @@ class Timer:
         torch.cuda.synchronize()
         self.cycles_per_s = n / max(a.elapsed_time(b) * 1e-3, 1e-9)
 
-    def run(self, launch, n_sets: int, steps: int, warmup: int):
+    def run(self, launch, n_sets: int, steps: int, warmup: int, warm_s=None):
         torch = self.torch
         if self.cycles_per_s is None:
             self._calibrate()
-        # Warm-up: at least `warmup` launches and at least WARM_S seconds of back-to-back
+        warm_s = self.warm_s if warm_s is None else warm_s
+        # Warm-up: at least `warmup` launches and at least warm_s seconds of back-to-back
         # launches, so that clocks have ramped up from the idle state before timing starts
         # (the first milliseconds after idle measured up to 15% slow).
         t_w = time.perf_counter()
         i = 0
-        while i < warmup or time.perf_counter() - t_w < WARM_S:
+        while i < warmup or time.perf_counter() - t_w < warm_s:
             launch(i % n_sets)
             i += 1
             if i % 64 == 0:
@@ -323,10 +388,6 @@ class Timer:
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
 
-        # Event pass: `fill` launches of the same kernel (at least 3 ms of GPU time) run ahead of
-        # the start event, so the queue is full and the clocks are up when timing starts. When
-        # the host enqueues more slowly than the GPU executes (short kernels), the stream is
-        # first held by a spin kernel until everything is enqueued.
         stream = torch.cuda.current_stream()
         fill = min(4000, max(8, int(3e-3 / max(wall / steps, 1e-7))))
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -359,13 +420,723 @@ def kernel_entry(name, nbytes, t, traffic=None, extra=None):
         e["traffic_bytes"] = traffic
     if extra:
         e.update(extra)
-    log(f"  {name:34s} {e['us_mean']:9.2f} us  {e['GBps']:8.1f} GB/s  "
+    log(f"  {name:36s} {e['us_mean']:9.2f} us  {e['GBps']:8.1f} GB/s  "
         f"{100 * e['frac_of_peak']:5.1f}% of 8 TB/s  (wall {e['us_wall_per_step']:.2f} us/step)")
     return e
 
 
 def sets_for(bytes_per_set: int, floor: int = 1 << 30, most: int = 64) -> int:
     return max(2, min(most, -(-floor // max(1, bytes_per_set)) + 1))
+
+
+class Bench:
+    def __init__(self, args):
+        import numpy as np
+        import torch
+        sys.path.insert(0, ROOT)
+        from __graft_entry__ import load_llmk
+        self.np, self.torch = np, torch
+        self.llmk = load_llmk()
+        import llmk.workloads as wl
+        self.wl = wl
+        self.args = args
+        self.dev = torch.device("cuda:0")
+        torch.cuda.set_device(self.dev)
+        self.timer = Timer(torch, args.warm_seconds)
+        self.traffic = read_traffic()
+        self.K, self.W = args.steps, args.warmup
+        self.kernels = {}
+        self.cpu_inputs = {}  # host copies of one input set per configuration
+        self.inv = torch.tensor(self.llmk.compute_rope_inv_freq(wl.HEAD_DIM, *wl.ROPE_ARGS),
+                                dtype=torch.float32, device=self.dev)
+
+    def mark(self, section: str) -> None:
+        self.llmk.empty_launch(MARK_BASE + SECTIONS.index(section), 64)
+
+    def run(self, launch, n_sets, steps=None, warmup=None):
+        return self.timer.run(launch, n_sets, self.K if steps is None else steps,
+                              self.W if warmup is None else warmup)
+
+    def free(self):
+        self.torch.cuda.synchronize()
+        self.torch.cuda.empty_cache()
+
+    # ------------------------------------------------------------------ configs 1-4
+    def config2(self):
+        wl, llmk = self.wl, self.llmk
+        rows, hidden = 8192, wl.HIDDEN
+        nbytes = wl.bytes_add_rmsnorm(rows, hidden)
+        R = sets_for(3 * rows * hidden * 2)
+        sets = [wl.add_rmsnorm_inputs(rows, hidden, seed=wl.SEED_BASE + 2 + 100 * i)
+                for i in range(R)]
+        w = sets[0]["w"]
+        self.cpu_inputs["add_rmsnorm_8192x2048"] = {
+            k: sets[0][k].cpu().numpy().view(self.np.uint16).copy() for k in ("residual", "x", "w")}
+
+        def launch(i):
+            s = sets[i]
+            llmk.add_rmsnorm(s["residual"], s["x"], w, s["out"], rows, hidden, wl.EPS)
+
+        self.mark("headline")
+        t = self.run(launch, R)
+        e = kernel_entry("add_rmsnorm [8192,2048]", nbytes, t,
+                         self.traffic.get("add_rmsnorm_8192x2048"), {"sets": R})
+        self.kernels["add_rmsnorm_8192x2048"] = e
+        del sets
+        self.free()
+        return t, nbytes, R
+
+    def config1(self):
+        wl, llmk = self.wl, self.llmk
+        hidden = wl.HIDDEN
+        sets1 = [wl.add_rmsnorm_inputs(16, hidden, seed=wl.SEED_BASE + 1 + 100 * i)
+                 for i in range(8)]
+        self.cpu_inputs["rmsnorm_16x2048"] = {
+            k: sets1[0][k].cpu().numpy().view(self.np.uint16).copy() for k in ("x", "w")}
+        self.mark("rmsnorm_16")
+        t = self.run(lambda i: llmk.rmsnorm(sets1[i]["x"], sets1[i]["w"], sets1[i]["out"], 16,
+                                            hidden, wl.EPS), 8)
+        self.kernels["rmsnorm_16x2048"] = kernel_entry(
+            "rmsnorm [16,2048]", wl.bytes_rmsnorm(16, hidden), t,
+            self.traffic.get("rmsnorm_16x2048"))
+        del sets1
+
+    def config3(self):
+        wl, llmk = self.wl, self.llmk
+        T = 8192
+        nb = wl.bytes_rope(T, wl.N_HEADS, wl.N_KV, wl.HEAD_DIM)
+        R3 = sets_for(nb // 2)
+        sets3 = [wl.rope_inputs(T, seed=wl.SEED_BASE + 3 + 100 * i, inv_freq=self.inv)
+                 for i in range(R3)]
+        self.cpu_inputs["rope_8192"] = {
+            "q": sets3[0]["q"].cpu().numpy().view(self.np.uint16).copy(),
+            "k": sets3[0]["k"].cpu().numpy().view(self.np.uint16).copy(),
+            "positions": sets3[0]["positions"].cpu().numpy().copy(),
+            "inv": self.inv.cpu().numpy().copy()}
+        self.mark("rope_8192")
+        t = self.run(lambda i: llmk.rope_apply(sets3[i]["q"], sets3[i]["k"],
+                                               sets3[i]["positions"], self.inv, T, wl.N_HEADS,
+                                               wl.N_KV, wl.HEAD_DIM), R3)
+        self.kernels["rope_8192"] = kernel_entry("rope_apply Q+K [8192 tokens]", nb, t,
+                                                 self.traffic.get("rope_8192"), {"sets": R3})
+        del sets3
+        self.free()
+
+    def config4a(self):
+        wl, llmk = self.wl, self.llmk
+        n = 8192 * wl.INTER
+        R4 = sets_for(wl.bytes_swiglu(n))
+        sets4 = [wl.swiglu_inputs(seed=wl.SEED_BASE + 4 + 100 * i) for i in range(R4)]
+        self.cpu_inputs["swiglu_8192x8192"] = {
+            k: sets4[0][k].cpu().numpy().view(self.np.uint16).copy() for k in ("gate", "up")}
+        self.mark("swiglu_8192")
+        t = self.run(lambda i: llmk.swiglu(sets4[i]["gate"], sets4[i]["up"], sets4[i]["out"], n),
+                     R4)
+        self.kernels["swiglu_8192x8192"] = kernel_entry(
+            "swiglu [8192,8192]", wl.bytes_swiglu(n), t, self.traffic.get("swiglu_8192x8192"),
+            {"sets": R4})
+        del sets4
+        self.free()
+
+    def config4b(self):
+        """Embedding gather of 8192 ids from [128256, 2048]. Four tables (2.1 GB) so a row read
+        by one launch is rarely still cached when its table comes round again. Returns one
+        table for the decode pass."""
+        wl, llmk = self.wl, self.llmk
+        hidden = wl.HIDDEN
+        tables = [wl.embedding_table(seed=wl.SEED_BASE + 40 + 100 * i) for i in range(4)]
+        R5 = 16
+        sets5 = [wl.embedding_inputs(8192, tables[i % 4], seed=wl.SEED_BASE + 41 + 100 * i)
+                 for i in range(R5)]
+        # the CPU gathers cycle through the 16 id sets too (from one table): repeating one set
+        # would serve its 33.5 MB of rows from the host's caches
+        self.cpu_inputs["embedding_8192"] = {
+            "table": tables[0].cpu().numpy().view(self.np.uint16),
+            "ids": [s["ids"].cpu().numpy().copy() for s in sets5]}
+        self.mark("embedding_8192")
+        t = self.run(lambda i: llmk.embedding_lookup(sets5[i]["table"], sets5[i]["ids"],
+                                                     sets5[i]["out"], 8192, hidden,
+                                                     check_indices=False), R5)
+        self.kernels["embedding_8192"] = kernel_entry(
+            "embedding_lookup 8192 of 128256", wl.bytes_embedding(8192, hidden), t,
+            self.traffic.get("embedding_8192"),
+            {"sets": R5, "tables": 4, "note": "ids uniform; ~3% duplicate rows per launch"})
+        table = tables[0]
+        del sets5, tables
+        self.free()
+        return table
+
+    # ------------------------------------------------------------------ config 5
+    def config5(self, table=None):
+        """The 16-layer non-GEMM decode pass over 256 sequences: two input sets (642 MB between
+        reuses, past the 256 MB MALL), each captured in a HIP graph and replayed alternately;
+        the same eagerly; then the breakdown: one graph per op type (the op's 16 launches of a
+        pass, the embedding's one) and graphs of empty kernels in the same launch shapes (the
+        launch floor), alternating between the two input sets likewise."""
+        wl, llmk, torch = self.wl, self.llmk, self.torch
+        if table is None:
+            table = wl.embedding_table(seed=wl.SEED_BASE + 40)
+        L, n = wl.LAYERS, 256
+        ps = [wl.decode_pass_inputs(self.inv, table=table, seed=wl.SEED_BASE + 5 + 100 * i)
+              for i in range(2)]
+        dps = [llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables,
+                                      p.positions, p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
+                                      n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
+                                      page_size=wl.PAGE, max_pages=p.max_pages, eps=wl.EPS)
+               for p in ps]
+        if not self.args.no_cpu:
+            self.cpu_inputs["decode_pass_16x256"] = cpu_pass_inputs(ps[0], wl)
+
+        def capture(fn):
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                fn()
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn()
+            return g
+
+        graphs = [capture(dp.run) for dp in dps]
+        steps, warm = max(20, self.K // 4), max(5, self.W // 4)
+        nb = wl.bytes_decode_pass(n, L)
+        self.mark("pass_graph")
+        t = self.run(lambda i: graphs[i].replay(), 2, steps, warm)
+        entry = kernel_entry("decode pass 16 layers x 256 (graph)", nb, t, None,
+                             {"launches": 1 + 3 * L, "layers": L, "seqs": n, "sets": 2,
+                              "note": "two input sets of 321 MB touched per pass, alternating "
+                                      "(> 256 MB MALL between reuses); one HIP graph of 49 "
+                                      "kernels per set"})
+        self.kernels["decode_pass_16x256"] = entry
+        self.mark("pass_eager")
+        t = self.run(lambda i: dps[i].run(), 2, steps, warm)
+        self.kernels["decode_pass_16x256_eager"] = kernel_entry(
+            "decode pass 16 layers x 256 (eager)", nb, t, None, {"sets": 2})
+
+        # ---- breakdown
+        def stage_fn(op, p):
+            def f():
+                if op == "embedding":
+                    llmk.embedding_lookup(p.table, p.token_ids, p.residual, n, wl.HIDDEN,
+                                          check_indices=False)
+                for lay in (p.per_layer if op != "embedding" else ()):
+                    if op == "add_rmsnorm":
+                        llmk.add_rmsnorm(p.residual, lay["x"], lay["norm_w"], lay["normed"], n,
+                                         wl.HIDDEN, wl.EPS)
+                    elif op == "rope_kv_scatter":
+                        llmk.rope_kv_scatter_batch(lay["q"], lay["k"], lay["v"], lay["k_pool"],
+                                                   lay["v_pool"], p.block_tables, p.positions,
+                                                   p.inv_freq, n, p.max_pages, wl.PAGE,
+                                                   wl.N_HEADS, wl.N_KV, wl.HEAD_DIM,
+                                                   check_indices=False)
+                    elif op == "swiglu":
+                        llmk.swiglu(lay["gate"], lay["up"], lay["act"], n * wl.INTER)
+            return f
+
+        def empty_fn(shapes):
+            def f():
+                for blocks, threads in shapes:
+                    llmk.empty_launch(blocks, threads)
+            return f
+
+        pass_shapes = [PASS_SHAPES["embedding"]] + [
+            PASS_SHAPES[op] for _ in range(L) for op in ("add_rmsnorm", "rope_kv_scatter",
+                                                         "swiglu")]
+        g_floor = capture(empty_fn(pass_shapes))
+        self.mark("pass_floor")
+        t_floor = self.run(lambda i: g_floor.replay(), 1, steps, warm)
+        bd = {"pass_us": entry["us_mean"], "launch_floor_49_us": round(t_floor["mean_s"] * 1e6, 3)}
+        log(f"    launch floor, 49 empty kernels in the pass's shapes: {bd['launch_floor_49_us']:.2f} us")
+        stages = {}
+        for op in ("embedding", "add_rmsnorm", "rope_kv_scatter", "swiglu"):
+            cnt = 1 if op == "embedding" else L
+            gs = [capture(stage_fn(op, p)) for p in ps]
+            self.mark(f"pass_stage_{op}")
+            t_op = self.run(lambda i: gs[i].replay(), 2, steps, warm)
+            ge = capture(empty_fn([PASS_SHAPES[op]] * cnt))
+            self.mark("pass_floor_stages")
+            t_e = self.run(lambda i: ge.replay(), 1, steps, warm)
+            us, us_e = t_op["mean_s"] * 1e6, t_e["mean_s"] * 1e6
+            stages[op] = {"launches": cnt, "us": round(us, 3), "us_per_launch": round(us / cnt, 3),
+                          "floor_us": round(us_e, 3), "floor_us_per_launch": round(us_e / cnt, 3),
+                          "work_us_per_launch": round((us - us_e) / cnt, 3)}
+            log(f"    stage {op:16s} {cnt:2d} launches {us:8.2f} us ({us / cnt:5.2f} per launch; "
+                f"empty kernels of the same shapes {us_e / cnt:5.2f})")
+            del gs, ge
+        bd["stages"] = stages
+        bd["sum_of_stages_us"] = round(sum(s["us"] for s in stages.values()), 3)
+        bd["pass_minus_floor_us"] = round(bd["pass_us"] - bd["launch_floor_49_us"], 3)
+        log(f"    sum of stages {bd['sum_of_stages_us']:.2f} us; pass {bd['pass_us']:.2f} us = "
+            f"launch floor {bd['launch_floor_49_us']:.2f} + work {bd['pass_minus_floor_us']:.2f}")
+        entry["breakdown"] = bd
+        del graphs, g_floor, dps, ps
+        self.free()
+
+    # ------------------------------------------------------------------ attention
+    def attention(self):
+        wl, llmk, np, torch = self.wl, self.llmk, self.np, self.torch
+        lens = wl.attention_lens()
+        if wl.bytes_attention(lens) != ATTN_BYTES_256:
+            raise RuntimeError(f"attention workload bytes {wl.bytes_attention(lens)} != "
+                               f"{ATTN_BYTES_256}")
+
+        def one(label, lens_b, R, section, quiet=False):
+            splits = llmk.choose_num_splits(lens_b.size, wl.N_KV, int(lens_b.max()))
+            sets6 = [wl.attention_inputs(lens_b, num_splits=splits,
+                                         seed=wl.SEED_BASE + 6 + 100 * i) for i in range(R)]
+
+            def launch_attn(i):
+                a = sets6[i]
+                llmk.attention_decode_fast(a["q"], a["k_pool"], a["v_pool"], a["block_tables"],
+                                           a["seq_lens"], a["out"], a["workspace"], a["n"],
+                                           a["max_pages"], wl.PAGE, wl.N_HEADS, wl.N_KV,
+                                           wl.HEAD_DIM, splits, check_indices=False)
+
+            self.mark(section)
+            t = self.run(launch_attn, R)
+            e = kernel_entry(f"attention {label}", wl.bytes_attention(lens_b), t,
+                             self.traffic.get(f"attention_decode_{label}"),
+                             {"sets": R, "num_splits": splits, "seqs": int(lens_b.size),
+                              "context_tokens": int(lens_b.sum()), "launches": 2})
+            del sets6
+            self.free()
+            return e
+
+        self.kernels["attention_decode_256"] = one("256", lens, 2, "attention_256")
+        self.kernels["attention_decode_16x2048"] = one("16x2048", np.full(16, 2048), 17,
+                                                       "attention_16x2048")
+        # batch sweep at a full 2048-position context, batch 1 = the latency of one sequence
+        # (ref: docs/attention_decode_batch_sweep.md:50-60, bench/bench_attention_compare.cu)
+        sweep = {}
+        for b in (1, 2, 4, 8, 16, 64, 256):
+            lb = np.full(b, 2048)
+            per_set = wl.bytes_attention(lb)
+            sweep[str(b)] = one(f"{b}x2048", lb, sets_for(per_set, most=256), "attention_sweep")
+        self.kernels["attention_decode_sweep_2048"] = sweep
+
+    def argmax(self):
+        wl, llmk, torch = self.wl, self.llmk, self.torch
+        R7, n7 = 17, 256
+        g7 = torch.Generator(device=self.dev)
+        g7.manual_seed(wl.SEED_BASE + 7)
+        logits = [torch.randn((n7, wl.VOCAB), generator=g7, device=self.dev).half()
+                  for _ in range(R7)]
+        am_out = torch.empty(n7, dtype=torch.int32, device=self.dev)
+        self.mark("argmax")
+        t = self.run(lambda i: llmk.argmax_rows(logits[i], am_out, n7, wl.VOCAB), R7)
+        self.kernels["argmax_256x128256"] = kernel_entry(
+            "argmax_rows [256,128256]", wl.bytes_argmax(n7, wl.VOCAB), t,
+            self.traffic.get("argmax_256x128256"), {"sets": R7})
+        del logits
+        self.free()
+
+    # ------------------------------------------------------------------ bandwidth ceilings
+    PROBE_NAMES = ("read", "copy", "read2", "inplace", "write")
+    PROBE_TRAFFIC = (1, 2, 3, 2, 1)  # bytes moved per byte of the probe's unit buffer
+
+    def probes(self):
+        """Sweep of every probe over grid and unroll at a 1 GiB unit buffer (two sets of
+        buffers, alternating), then each kernel's own mix at its own byte count."""
+        llmk, torch = self.llmk, self.torch
+        nb = 1 << 30
+        bufs = [[torch.empty(nb, dtype=torch.uint8, device=self.dev) for _ in range(3)]
+                for _ in range(2)]
+        for s in bufs:
+            for t in s:
+                t.random_(0, 256)
+        sweep = {}
+        self.mark("probe_sweep")
+        for mode, name in enumerate(self.PROBE_NAMES):
+            res = []
+            for blocks in (0, 1024, 2048, 4096, 8192):
+                for unroll in (1, 2, 4, 8):
+                    def launch(i, mode=mode, blocks=blocks, unroll=unroll):
+                        a, b, d = bufs[i]
+                        llmk.bw_probe(mode, d if mode != 0 else a, nb, a=a, b=b, blocks=blocks,
+                                      unroll=unroll)
+                    t = self.timer.run(launch, 2, 10, 3, warm_s=0.02)
+                    gbs = self.PROBE_TRAFFIC[mode] * nb / t["mean_s"] / 1e9
+                    res.append({"blocks": blocks, "unroll": unroll, "GBps": round(gbs, 1)})
+            best = max(res, key=lambda r: r["GBps"])
+            sweep[name] = {"best": best, "one_pass_unroll4": next(
+                r for r in res if r["blocks"] == 0 and r["unroll"] == 4)}
+            log(f"  probe {name:8s} best {best['GBps']:7.1f} GB/s ({100 * best['GBps'] / PEAK_GBS:4.1f}%)"
+                f" at blocks {best['blocks']} unroll {best['unroll']}; GB/s by blocks (0 = one "
+                f"pass) x unroll 1/2/4/8: " + "; ".join(
+                    f"{bl}: " + "/".join(f"{r['GBps']:.0f}" for r in res if r["blocks"] == bl)
+                    for bl in (0, 1024, 2048, 4096, 8192)))
+        del bufs
+        self.free()
+        self.kernels["probe_sweep_1GiB"] = sweep
+        return sweep
+
+    def kernel_ceilings(self, sweep):
+        """Each kernel's traffic mix at its own byte count and rotation, with the best sweep
+        setting of that mix and with one pass of unroll 4 (the kernels' launch style); the
+        faster is the kernel's ceiling."""
+        llmk, torch, wl = self.llmk, self.torch, self.wl
+        # (kernel label, probe mode, bytes of the unit buffer, sets)
+        mixes = [("add_rmsnorm_8192x2048", 1, 134221824 // 2, 12),
+                 ("rope_8192", 3, 83918976 // 2, 27),
+                 ("swiglu_8192x8192", 2, 402653184 // 3, 4),
+                 ("embedding_8192", 1, 67141632 // 2, 16),
+                 ("argmax_256x128256", 0, wl.bytes_argmax(256, wl.VOCAB), 17),
+                 ("attention_decode_256", 0, ATTN_BYTES_256, 2)]
+        self.mark("probe_kernels")
+        out = {}
+        for label, mode, unit, R in mixes:
+            if label not in self.kernels:
+                continue
+            unit -= unit % 16
+            bufs = [[torch.empty(unit, dtype=torch.uint8, device=self.dev)
+                     for _ in range(3 if mode == 2 else (1 if mode in (0, 3) else 2))]
+                    for _ in range(R)]
+            name = self.PROBE_NAMES[mode]
+            best = sweep[name]["best"]
+            res = []
+            for blocks, unroll in ((best["blocks"], best["unroll"]), (0, 4)):
+                def launch(i, mode=mode, blocks=blocks, unroll=unroll):
+                    s = bufs[i]
+                    if mode == 0:
+                        llmk.bw_probe(0, s[0], unit, a=s[0], blocks=blocks, unroll=unroll)
+                    elif mode == 3:
+                        llmk.bw_probe(3, s[0], unit, blocks=blocks, unroll=unroll)
+                    elif mode == 1:
+                        llmk.bw_probe(1, s[1], unit, a=s[0], blocks=blocks, unroll=unroll)
+                    else:
+                        llmk.bw_probe(2, s[2], unit, a=s[0], b=s[1], blocks=blocks,
+                                      unroll=unroll)
+                t = self.run(launch, R)
+                res.append((self.PROBE_TRAFFIC[mode] * unit / t["mean_s"] / 1e9, blocks, unroll,
+                            t["mean_s"] * 1e6))
+            gbs, blocks, unroll, us = max(res)
+            k = self.kernels[label]
+            c = {"mix": name, "GBps": round(gbs, 1), "us": round(us, 3), "blocks": blocks,
+                 "unroll": unroll, "frac_of_peak": round(gbs / PEAK_GBS, 4),
+                 "kernel_frac_of_ceiling": round(k["GBps"] / gbs, 4)}
+            k["ceiling"] = c
+            out[label] = c
+            log(f"  ceiling {label:24s} {name:8s} {gbs:7.1f} GB/s ({100 * gbs / PEAK_GBS:4.1f}%);"
+                f" kernel at {100 * k['GBps'] / gbs:5.1f}% of it")
+            del bufs
+            self.free()
+        return out
+
+    def copy_probe(self):
+        llmk, torch = self.llmk, self.torch
+        nb = 1 << 30
+        bufs = [torch.empty(nb, dtype=torch.uint8, device=self.dev) for _ in range(4)]
+        self.mark("copy_1GiB")
+        t = self.run(lambda i: llmk.copy_bytes(bufs[2 * (i % 2)], bufs[2 * (i % 2) + 1], nb), 2,
+                     max(20, self.K // 4), 5)
+        self.kernels["copy_1GiB"] = kernel_entry("copy probe 1 GiB", 2 * nb, t,
+                                                 self.traffic.get("copy_1GiB"))
+        del bufs
+        self.free()
+
+    # ------------------------------------------------------------------ CPU baselines
+    def cpu_baselines(self, seconds):
+        """The scalar C oracle (oracle/, test infrastructure) of each configuration's work on
+        host copies of the configuration's first input set: all cores of the process's CPU
+        affinity (rows split over threads, identical results), then one core. Outputs are
+        preallocated and in-place operands keep being updated, so no copy or first-touch page
+        fault is inside the timed loops."""
+        import numpy as np
+        sys.path.insert(0, ROOT)
+        import oracle
+        lib = oracle.lib()
+        wl = self.wl
+        u16 = ctypes.POINTER(ctypes.c_uint16)
+        i32 = ctypes.POINTER(ctypes.c_int32)
+        f32 = ctypes.POINTER(ctypes.c_float)
+
+        def P(a, t=u16):
+            return a.ctypes.data_as(t)
+
+        threads = len(os.sched_getaffinity(0))
+        info = {"cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+                "affinity_cores": threads, "threads_used": threads}
+
+        def timed(fn, budget, first=True):
+            if first:
+                fn()  # first call outside the timed loop (touches the output pages)
+            reps, t0 = 0, time.perf_counter()
+            while True:
+                fn()
+                reps += 1
+                el = time.perf_counter() - t0
+                if el >= budget:
+                    return reps, el
+
+        def figure(label, nbytes, make, sample):
+            if label not in self.cpu_inputs:
+                return
+            fn_all, fn_one = make(threads), make(1)
+            reps, el = timed(fn_all, seconds * 0.7)
+            reps1, el1 = timed(fn_one, seconds * 0.3, first=False)
+            v, v1 = nbytes * reps / el / 1e9, nbytes * reps1 / el1 / 1e9
+            c = {"value": round(v, 3), "unit": "GB/s", "us": round(el / reps * 1e6, 1),
+                 "cores": threads, "kind": "port",
+                 "sample": f"{reps} {sample} in {el:.1f} s, the scalar C oracle over {threads} "
+                           f"threads", "one_core": {"value": round(v1, 3), "unit": "GB/s",
+                                                    "us": round(el1 / reps1 * 1e6, 1),
+                                                    "cores": 1,
+                                                    "sample": f"{reps1} in {el1:.1f} s"}}
+            if label in self.kernels:
+                self.kernels[label]["cpu"] = c
+                c["gpu_over_cpu"] = round(self.kernels[label]["GBps"] / max(v, 1e-9), 1)
+            log(f"  CPU oracle {label:26s} {v:7.3f} GB/s on {threads} threads, {v1:7.3f} on 1 "
+                f"({el / reps * 1e6:.0f} us per call)")
+            return c
+
+        out = {}
+        eps, H = wl.EPS, wl.HIDDEN
+        d = self.cpu_inputs.get("add_rmsnorm_8192x2048")
+        if d:
+            o = np.empty_like(d["x"])
+
+            def mk2(th):
+                return lambda: lib.or_add_rmsnorm_mt(P(d["residual"]), P(d["x"]), P(d["w"]), P(o),
+                                                     8192, H, eps, th)
+            out["add_rmsnorm_8192x2048"] = figure("add_rmsnorm_8192x2048",
+                                                  wl.bytes_add_rmsnorm(8192, H), mk2,
+                                                  "full [8192,2048] add_rmsnorm passes")
+        d = self.cpu_inputs.get("rmsnorm_16x2048")
+        if d:
+            o = np.empty_like(d["x"])
+
+            def mk1(th):  # 16 rows: one thread per row at most; the scalar function on one core
+                return lambda: lib.or_rmsnorm(P(d["x"]), P(d["w"]), P(o), 16, H, eps)
+            c = figure("rmsnorm_16x2048", wl.bytes_rmsnorm(16, H), mk1, "[16,2048] rmsnorm calls")
+            if c:
+                c["cores"] = 1
+                c["sample"] += " (single-threaded: 16 rows)"
+            out["rmsnorm_16x2048"] = c
+        d = self.cpu_inputs.get("rope_8192")
+        if d:
+            def mk3(th):
+                return lambda: lib.or_rope_apply_mt(P(d["q"]), P(d["k"]), P(d["positions"], i32),
+                                                    P(d["inv"], f32), 8192, wl.N_HEADS, wl.N_KV,
+                                                    wl.HEAD_DIM, th)
+            out["rope_8192"] = figure("rope_8192", wl.bytes_rope(8192, wl.N_HEADS, wl.N_KV,
+                                                                 wl.HEAD_DIM), mk3,
+                                      "in-place RoPE passes over Q [8192,32,64] + K [8192,8,64]")
+        d = self.cpu_inputs.get("swiglu_8192x8192")
+        if d:
+            o = np.empty_like(d["gate"])
+
+            def mk4(th):
+                return lambda: lib.or_swiglu_mt(P(d["gate"]), P(d["up"]), P(o), d["gate"].size, th)
+            out["swiglu_8192x8192"] = figure("swiglu_8192x8192", wl.bytes_swiglu(d["gate"].size),
+                                             mk4, "[8192,8192] SwiGLU passes")
+        d = self.cpu_inputs.get("embedding_8192")
+        if d:
+            o = np.empty((8192, H), np.uint16)
+
+            def mk5(th):
+                it = [0]
+
+                def f():
+                    ids = d["ids"][it[0] % len(d["ids"])]
+                    it[0] += 1
+                    lib.or_embedding_lookup_mt(P(d["table"]), P(ids, i32), P(o), 8192, H, th)
+                return f
+            out["embedding_8192"] = figure("embedding_8192", wl.bytes_embedding(8192, H), mk5,
+                                           f"gathers of 8192 rows from [128256,2048] (cycling "
+                                           f"through {len(d['ids'])} id sets)")
+        h = self.cpu_inputs.get("decode_pass_16x256")
+        if h is not None:
+            out["decode_pass_16x256"] = figure(
+                "decode_pass_16x256", wl.bytes_decode_pass(h["n"], len(h["layers"])),
+                cpu_decode_pass(h, lib, wl, P, i32, f32),
+                "16-layer passes over 256 sequences (embedding; add+RMSNorm, RoPE + K/V "
+                "scatter, SwiGLU per layer; each sequence's pool page remapped into a 256-page "
+                "host pool, the same rows moved)")
+        out["info"] = info
+        self.cpu_info = info
+        return out
+
+    # ------------------------------------------------------------------ the engine
+    def decode_step(self, n_seqs=256):
+        wl, llmk, torch, np = self.wl, self.llmk, self.torch, self.np
+        import importlib
+        weights = importlib.import_module("llmk.weights")
+        cfg = llmk.ModelConfig()
+        lens = wl.attention_lens(n_seqs)
+        tokens, pos, tables, used = wl.decode_step_rows(lens)
+        n = lens.size
+        eng = llmk.Engine(cfg, max_rows=n, max_pages=128, num_pages=used)
+        w = weights.random_weights(cfg, wl.SEED_BASE + 9, device=self.dev)
+        eng.set_weights(*weights.engine_layers(w, cfg))
+        del w
+        g = torch.Generator(device=self.dev)
+        g.manual_seed(wl.SEED_BASE + 10)
+        fill = torch.randn(used * wl.PAGE * wl.N_KV * wl.HEAD_DIM, generator=g,
+                           device=self.dev).half()
+        for l in range(cfg.n_layers):
+            for which in (llmk.BUF_K_POOL, llmk.BUF_V_POOL):
+                eng.write_pool(which, l, fill)
+        del fill
+        self.free()
+        eng.tune(n)     # time hipBLASLt's candidates for this batch's projection shapes
+        eng.set_rows(tokens, pos, tables)
+        eng.forward(n)  # eager once before capture
+        torch.cuda.synchronize()
+        if not torch.isfinite(eng.logits(n).float()).all():
+            raise RuntimeError("decode step produced non-finite logits")
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            eng.forward(n, stream=s)
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            eng.forward(n)
+        self.mark("step_256" if n_seqs == 256 else "step_8")
+        t = self.run(lambda i: graph.replay(), 1, max(20, self.K // 4), max(5, self.W // 4))
+        nbytes = wl.bytes_decode_step(lens)
+        path = ("fused few-rows projections (libllmk) with the norms, RoPE + scatter, SwiGLU and "
+                "residual adds inside them" if n <= llmk.LINEAR_ROWS_MAX else
+                "hipBLASLt projections + libllmk kernels")
+        e = kernel_entry(f"decode step 1B, {n} seqs (graph)", nbytes, t, None, {
+            "tokens_per_s": round(n / t["mean_s"], 1), "seqs": int(n),
+            "context_tokens": int(lens.sum()), "layers": cfg.n_layers,
+            "note": f"engine forward pass: {path}, one HIP graph; bytes = sum of the step's "
+                    "kernels' algorithmic bytes (weights 2.47 GB, KV cache reads, activations "
+                    "between kernels)"})
+        log(f"    -> {e['tokens_per_s']:.0f} tokens/s")
+        eng.close()
+        del graph
+        self.free()
+        self.kernels[f"decode_step_1b_{n}"] = e
+
+    def scheduler(self):
+        """The reference's scheduler benchmark on the engine (Llama-3.2-1B shape, seeded random
+        weights): 24 requests (prompts of 5 to 402 tokens, 32 new tokens each, one eligible every
+        2 iterations), 256 pages of 16, one request at a time and up to 8 at once, two rounds
+        each as the reference runs them (ref: tests/test_scheduler.cu:14-76). words/s = new
+        tokens over the scheduler's own wall clock (first iteration to last retirement), as the
+        reference reports it. Decode steps of each batch size run from the engine's HIP graph
+        cache."""
+        wl, llmk, torch, np = self.wl, self.llmk, self.torch, self.np
+        import importlib
+        weights = importlib.import_module("llmk.weights")
+        cfg = llmk.ModelConfig()
+        max_len = max(wl.SCHED_PROMPT_LENS) + wl.SCHED_NEW
+        max_pages = (max_len + wl.PAGE - 1) // wl.PAGE
+        max_rows = 512  # the longest prompt (402 tokens) prefills in one pass
+        eng = llmk.Engine(cfg, max_rows=max_rows, max_pages=max_pages, num_pages=wl.SCHED_PAGES)
+        # A wide embedding (std 0.5) makes the logits peaked, so that the greedy tokens do not
+        # hinge on last-bit differences: a sequence's bits depend on its batch (the attention's
+        # split count follows the batch size), as cuBLAS results do in the reference.
+        w = weights.random_weights(cfg, wl.SEED_BASE + 9, device=self.dev, embed_std=0.5)
+        eng.set_weights(*weights.engine_layers(w, cfg))
+        del w
+        self.free()
+        stream = torch.cuda.Stream()
+        model = eng.sched_model(stream)
+        reqs = wl.scheduler_requests()
+        order = np.random.default_rng(wl.SEED_BASE + 12).permutation(
+            wl.SCHED_PAGES).astype(np.int32)
+
+        def run(rs, max_running):
+            pages = llmk.PageAllocator(wl.SCHED_PAGES)
+            pages.set_free_list(order)
+            outs, stats, _ = llmk.run_scheduler(rs, max_running, max_pages, wl.PAGE, pages, model)
+            if pages.num_free() != wl.SCHED_PAGES:
+                raise RuntimeError("scheduler run leaked pages")
+            return outs, stats
+
+        self.mark("sched")
+        run(reqs[:2], wl.SCHED_MAX_RUNNING)  # warm-up, as the reference does
+        run(reqs[:wl.SCHED_MAX_RUNNING], wl.SCHED_MAX_RUNNING)  # captures the decode graphs
+        rounds = []
+        outputs = {}
+        for rnd in (1, 2):
+            for mr in (1, wl.SCHED_MAX_RUNNING):
+                outs, st = run(reqs, mr)
+                if mr in outputs and outputs[mr] != outs:
+                    raise RuntimeError("scheduler outputs changed between rounds")
+                outputs[mr] = outs
+                wps = st["total_words"] / (st["total_ms"] * 1e-3)
+                rounds.append({"round": rnd, "max_running": mr,
+                               "decode_steps": st["decode_steps"],
+                               "mean_batch": round(st["mean_batch"], 2),
+                               "total_ms": round(st["total_ms"], 2),
+                               "prefill_ms": round(st["prefill_ms"], 2),
+                               "decode_ms": round(st["decode_ms"], 2),
+                               "words_per_s": round(wps, 1)})
+                log(f"  scheduler round {rnd}, up to {mr} at once: {st['decode_steps']} decode "
+                    f"steps, mean batch {st['mean_batch']:.1f}, {st['total_ms']:.1f} ms, "
+                    f"{wps:.0f} words/s")
+        if outputs[1] != outputs[wl.SCHED_MAX_RUNNING]:
+            raise RuntimeError("batched and one-at-a-time scheduler outputs differ")
+        best = {mr: max(r["words_per_s"] for r in rounds if r["max_running"] == mr)
+                for mr in (1, wl.SCHED_MAX_RUNNING)}
+        eng.close()
+        self.free()
+        self.kernels["scheduler_24x32_1b"] = {
+            "label": "continuous batching, 24 requests x 32 new tokens (Llama-3.2-1B shape)",
+            "words_per_s": best[wl.SCHED_MAX_RUNNING], "words_per_s_one_at_a_time": best[1],
+            "gain": round(best[wl.SCHED_MAX_RUNNING] / best[1], 2), "rounds": rounds,
+            "note": "reference on an RTX 4050 Laptop: 249 words/s up to 8 at once, 60 one at a "
+                    "time (docs/scheduler_results.md); outputs identical in both modes"}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_pass_inputs(p, wl) -> dict:
+    """Host copies of a decode-pass input set for the CPU baseline. Each sequence's pool page is
+    remapped to page b of a 256-page host pool: the rows the pass moves are the same, and the
+    8.6 GB of device pools, almost all untouched by one pass, are not copied."""
+    import numpy as np
+    n, kvdim = p.n, wl.N_KV * wl.HEAD_DIM
+    pos = (p.lens - 1).astype(np.int32)
+    tables = np.zeros((n, p.max_pages), np.int32)
+    tables[np.arange(n), pos // wl.PAGE] = np.arange(n, dtype=np.int32)
+    return {"n": n, "max_pages": p.max_pages, "pos": pos, "tables": tables,
+            "table": p.table.cpu().numpy().view(np.uint16),
+            "ids": p.token_ids.cpu().numpy().astype(np.int32),
+            "inv": p.inv_freq.cpu().numpy().astype(np.float32),
+            "kpool": np.full(n * wl.PAGE * kvdim, wl.POISON, np.uint16),
+            "vpool": np.full(n * wl.PAGE * kvdim, wl.POISON, np.uint16),
+            "residual": np.empty((n, wl.HIDDEN), np.uint16),
+            "layers": [{k: v.cpu().numpy().view(np.uint16).copy() for k, v in lay.items()
+                        if k not in ("k_pool", "v_pool")} for lay in p.per_layer]}
+
+
+def cpu_decode_pass(h, lib, wl, P, i32, f32):
+    """A maker of the CPU decode pass: the same ops as llmk_decode_nongemm_pass (embedding; per
+    layer add+RMSNorm, RoPE of Q and K, K and V scattered into the pools, SwiGLU) by the scalar
+    oracle, on the host copies of cpu_pass_inputs."""
+    n, H, kvdim = h["n"], wl.HIDDEN, wl.N_KV * wl.HEAD_DIM
+
+    def make(th):
+        def f():
+            lib.or_embedding_lookup_mt(P(h["table"]), P(h["ids"], i32), P(h["residual"]), n, H,
+                                       th)
+            for lay in h["layers"]:
+                lib.or_add_rmsnorm_mt(P(h["residual"]), P(lay["x"]), P(lay["norm_w"]),
+                                      P(lay["normed"]), n, H, wl.EPS, th)
+                lib.or_rope_apply_mt(P(lay["q"]), P(lay["k"]), P(h["pos"], i32),
+                                     P(h["inv"], f32), n, wl.N_HEADS, wl.N_KV, wl.HEAD_DIM, th)
+                lib.or_kv_scatter_batch(P(lay["k"]), P(h["kpool"]), P(h["tables"], i32),
+                                        P(h["pos"], i32), n, h["max_pages"], wl.PAGE, kvdim)
+                lib.or_kv_scatter_batch(P(lay["v"]), P(h["vpool"]), P(h["tables"], i32),
+                                        P(h["pos"], i32), n, h["max_pages"], wl.PAGE, kvdim)
+                lib.or_swiglu_mt(P(lay["gate"]), P(lay["up"]), P(lay["act"]), n * wl.INTER, th)
+        return f
+    return make
 
 
 def main() -> int:
@@ -383,372 +1154,67 @@ def main() -> int:
         print(f"bench.py measures one GPU only (the kernels are single-GPU; this build has no "
               f"multi-GPU path): --gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
-    import numpy as np
     import torch
-
-    sys.path.insert(0, ROOT)
-    from __graft_entry__ import load_llmk
-    llmk = load_llmk()
-    import llmk.workloads as wl
-
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    timer = Timer(torch)
-    traffic = read_traffic()
+    b = Bench(args)
     K, W = args.steps, args.warmup
-    log(f"device: {torch.cuda.get_device_name(dev)}  steps={K} warmup={W}")
-    kernels = {}
+    log(f"device: {torch.cuda.get_device_name(b.dev)}  steps={K} warmup={W}")
+    what = args.kernels
+    allk = what in ("all", "kernels")
+    t_head, nbytes, R = b.config2()
+    if allk or what == "configs":
+        b.config1()
+        b.config3()
+        b.config4a()
+    table = b.config4b() if allk or what == "configs" else None
+    if allk or what in ("configs", "pass"):
+        b.config5(table)
+    del table
+    if allk or what == "attn":
+        b.attention()
+    if allk:
+        b.argmax()
+    if what in ("all", "step"):
+        b.decode_step(256)
+    if what in ("all", "step8"):
+        b.decode_step(8)
+    if what in ("all", "sched"):
+        b.scheduler()
+    if allk or what in ("probe", "configs"):
+        sweep = b.probes()
+        b.kernel_ceilings(sweep)
+    b.copy_probe()
+    b.mark("end")
+    torch.cuda.synchronize()
 
-    # ---------------- headline: fused residual add + RMSNorm [8192, 2048] ----------------
-    rows, hidden = 8192, wl.HIDDEN
-    nbytes = wl.bytes_add_rmsnorm(rows, hidden)
-    R = sets_for(3 * rows * hidden * 2)
-    sets = [wl.add_rmsnorm_inputs(rows, hidden, seed=wl.SEED_BASE + 2 + 100 * i) for i in range(R)]
-    w = sets[0]["w"]
-
-    def launch_add_rmsnorm(i):
-        s = sets[i]
-        llmk.add_rmsnorm(s["residual"], s["x"], w, s["out"], rows, hidden, wl.EPS)
-
-    t = timer.run(launch_add_rmsnorm, R, K, W)
-    head = kernel_entry("add_rmsnorm [8192,2048]", nbytes, t, traffic.get("add_rmsnorm_8192x2048"),
-                        {"sets": R})
-    kernels["add_rmsnorm_8192x2048"] = head
-    headline_wall = t["wall_s"]
-    cpu_inputs = {k: sets[0][k].cpu().contiguous() for k in ("residual", "x", "w")}
-    del sets
-    torch.cuda.empty_cache()
-
-    if args.kernels == "step":
-        kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W))
-    if args.kernels == "step8":
-        kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W, n_seqs=8))
-    if args.kernels == "sched":
-        kernels.update(bench_scheduler(llmk, wl, torch, np, dev))
-
-    if args.kernels == "all":
-        # config 1: RMSNorm [16, 2048] (the reference's CPU-plumbing case, on the GPU)
-        sets1 = [wl.add_rmsnorm_inputs(16, hidden, seed=wl.SEED_BASE + 1 + 100 * i)
-                 for i in range(8)]
-        t = timer.run(lambda i: llmk.rmsnorm(sets1[i]["x"], sets1[i]["w"], sets1[i]["out"], 16,
-                                             hidden, wl.EPS), 8, K, W)
-        kernels["rmsnorm_16x2048"] = kernel_entry("rmsnorm [16,2048]",
-                                                  wl.bytes_rmsnorm(16, hidden), t,
-                                                  traffic.get("rmsnorm_16x2048"))
-        del sets1
-
-        # config 3: RoPE, Q [8192,32,64] + K [8192,8,64], positions < 131072
-        inv = torch.tensor(llmk.compute_rope_inv_freq(wl.HEAD_DIM, *wl.ROPE_ARGS),
-                           dtype=torch.float32, device=dev)
-        T = 8192
-        R3 = sets_for(wl.bytes_rope(T, wl.N_HEADS, wl.N_KV, wl.HEAD_DIM) // 2)
-        sets3 = [wl.rope_inputs(T, seed=wl.SEED_BASE + 3 + 100 * i, inv_freq=inv)
-                 for i in range(R3)]
-        t = timer.run(lambda i: llmk.rope_apply(sets3[i]["q"], sets3[i]["k"],
-                                                sets3[i]["positions"], inv, T, wl.N_HEADS,
-                                                wl.N_KV, wl.HEAD_DIM), R3, K, W)
-        kernels["rope_8192"] = kernel_entry(
-            "rope_apply Q+K [8192 tokens]", wl.bytes_rope(T, wl.N_HEADS, wl.N_KV, wl.HEAD_DIM),
-            t, traffic.get("rope_8192"), {"sets": R3})
-        del sets3
-
-        # config 4a: SwiGLU [8192, 8192]
-        n = 8192 * wl.INTER
-        R4 = sets_for(wl.bytes_swiglu(n))
-        sets4 = [wl.swiglu_inputs(seed=wl.SEED_BASE + 4 + 100 * i) for i in range(R4)]
-        t = timer.run(lambda i: llmk.swiglu(sets4[i]["gate"], sets4[i]["up"], sets4[i]["out"], n),
-                      R4, K, W)
-        kernels["swiglu_8192x8192"] = kernel_entry("swiglu [8192,8192]", wl.bytes_swiglu(n), t,
-                                                   traffic.get("swiglu_8192x8192"), {"sets": R4})
-        del sets4
-        torch.cuda.empty_cache()
-
-        # config 4b: embedding gather of 8192 ids from [128256, 2048]. Four tables (2.1 GB)
-        # so a row read by one launch is rarely still cached when its table comes round again.
-        tables = [wl.embedding_table(seed=wl.SEED_BASE + 40 + 100 * i) for i in range(4)]
-        R5 = 16
-        sets5 = [wl.embedding_inputs(8192, tables[i % 4], seed=wl.SEED_BASE + 41 + 100 * i)
-                 for i in range(R5)]
-        t = timer.run(lambda i: llmk.embedding_lookup(sets5[i]["table"], sets5[i]["ids"],
-                                                      sets5[i]["out"], 8192, hidden,
-                                                      check_indices=False), R5, K, W)
-        kernels["embedding_8192"] = kernel_entry(
-            "embedding_lookup 8192 of 128256", wl.bytes_embedding(8192, hidden), t,
-            traffic.get("embedding_8192"), {"sets": R5, "tables": 4,
-                                       "note": "ids uniform; ~3% duplicate rows per launch"})
-        table = tables[0]
-        del sets5, tables
-
-        # config 5: decode-step non-GEMM pass, 16 layers x 256 sequences, in a HIP graph
-        p = wl.decode_pass_inputs(inv, table=table)
-        dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables,
-                                    p.positions, p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
-                                    n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
-                                    page_size=wl.PAGE, max_pages=p.max_pages, eps=wl.EPS)
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            dp.run()
-        torch.cuda.current_stream().wait_stream(s)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            dp.run()
-        t = timer.run(lambda i: graph.replay(), 1, max(20, K // 4), max(5, W // 4))
-        kernels["decode_pass_16x256"] = kernel_entry(
-            "decode pass 16 layers x 256 (graph)", wl.bytes_decode_pass(256, 16), t, None,
-            {"launches": 1 + 3 * 16, "layers": 16, "seqs": 256,
-             "note": "footprint 321 MB (> 256 MB MALL); one HIP graph of 49 kernels"})
-        t = timer.run(lambda i: dp.run(), 1, max(20, K // 4), max(5, W // 4))
-        kernels["decode_pass_16x256_eager"] = kernel_entry(
-            "decode pass 16 layers x 256 (eager)", wl.bytes_decode_pass(256, 16), t)
-        del p, dp, graph, table
-        torch.cuda.empty_cache()
-
-        # decode attention over the paged pool (the pool's consumer): 256 sequences with
-        # lengths uniform in [1, 2048], and the reference's bench shape, 16 sequences x 2048
-        # (ref: bench/bench_attention_compare.cu). Split count: choose_num_splits' default.
-        lens = wl.attention_lens()
-        nb_attn = wl.bytes_attention(lens)
-        if nb_attn != ATTN_BYTES_256:
-            raise RuntimeError(f"attention workload bytes {nb_attn} != {ATTN_BYTES_256}")
-        for label, lens_b, R6 in (("attention_decode_256", lens, 2),
-                                  ("attention_decode_16x2048", np.full(16, 2048), 17)):
-            splits = llmk.choose_num_splits(lens_b.size, wl.N_KV, int(lens_b.max()))
-            sets6 = [wl.attention_inputs(lens_b, num_splits=splits,
-                                         seed=wl.SEED_BASE + 6 + 100 * i) for i in range(R6)]
-
-            def launch_attn(i, sets6=sets6, splits=splits):
-                a = sets6[i]
-                llmk.attention_decode_fast(a["q"], a["k_pool"], a["v_pool"], a["block_tables"],
-                                           a["seq_lens"], a["out"], a["workspace"], a["n"],
-                                           a["max_pages"], wl.PAGE, wl.N_HEADS, wl.N_KV,
-                                           wl.HEAD_DIM, splits, check_indices=False)
-
-            t = timer.run(launch_attn, R6, K, W)
-            kernels[label] = kernel_entry(
-                f"attention_decode_fast {label.split('_')[-1]}", wl.bytes_attention(lens_b), t,
-                traffic.get(label), {"sets": R6, "num_splits": splits, "seqs": int(lens_b.size),
-                                     "context_tokens": int(lens_b.sum()),
-                                     "launches": 2, "note": "page-balanced split + merge"})
-            del sets6
-            torch.cuda.empty_cache()
-
-        # argmax over the logits of a decode batch: [256, 128256] (ref: kernels/argmax.cu,
-        # engine/batched.cu:150). 17 sets of 65.7 MB rotate through more than 1 GB.
-        R7, n7 = 17, 256
-        g7 = torch.Generator(device=dev)
-        g7.manual_seed(wl.SEED_BASE + 7)
-        logits = [torch.randn((n7, wl.VOCAB), generator=g7, device=dev).half()
-                  for _ in range(R7)]
-        am_out = torch.empty(n7, dtype=torch.int32, device=dev)
-        t = timer.run(lambda i: llmk.argmax_rows(logits[i], am_out, n7, wl.VOCAB), R7, K, W)
-        kernels["argmax_256x128256"] = kernel_entry(
-            "argmax_rows [256,128256]", wl.bytes_argmax(n7, wl.VOCAB), t,
-            traffic.get("argmax_256x128256"), {"sets": R7})
-        del logits
-        torch.cuda.empty_cache()
-
-        # the whole decode step of the engine (Llama-3.2-1B shape, seeded random weights):
-        # 256 sequences with context lengths uniform in [1, 2048] (the attention workload), one
-        # new token each, every layer's K/V pool pre-filled for the cached positions; one HIP
-        # graph per step (ref: engine/batched.cu:81-120, model_decode_batch_greedy :146-150)
-        kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W))
-        # the same with 8 sequences: the fused few-rows pass (projections streaming the weights
-        # with the norms, RoPE + scatter, SwiGLU and residual adds inside them)
-        kernels.update(bench_decode_step(llmk, wl, timer, torch, np, dev, K, W, n_seqs=8))
-
-        # continuous batching on the engine: the reference's scheduler workload, one request
-        # at a time and up to 8 at once (ref: tests/test_scheduler.cu, engine/scheduler.cu)
-        kernels.update(bench_scheduler(llmk, wl, torch, np, dev))
-
-        # copy probe: practical HBM ceiling (ref: bench/bandwidth.cu)
-        nb = 1 << 30
-        bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(4)]
-        t = timer.run(lambda i: llmk.copy_bytes(bufs[2 * (i % 2)], bufs[2 * (i % 2) + 1], nb),
-                      2, max(20, K // 4), 5)
-        kernels["copy_1GiB"] = kernel_entry("copy probe 1 GiB", 2 * nb, t,
-                                            traffic.get("copy_1GiB"))
-        del bufs
-
-    # ---------------- CPU baseline: the scalar oracle on the host cores ----------------
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cpu_inputs, rows, hidden, nbytes, args.cpu_seconds, wl.EPS)
+        cpus = b.cpu_baselines(args.cpu_seconds)
+        head_cpu = cpus.get("add_rmsnorm_8192x2048")
+        if head_cpu:
+            cpu = {k: v for k, v in head_cpu.items() if k != "gpu_over_cpu"}
+            cpu.update(b.cpu_info)
 
-    value = nbytes * K / headline_wall / 1e9
+    head = b.kernels["add_rmsnorm_8192x2048"]
+    value = nbytes * K / t_head["wall_s"] / 1e9
     rec = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
-        "warmup": W, "ms_per_step": round(headline_wall / K * 1e3, 5),
+        "warmup": W, "ms_per_step": round(t_head["wall_s"] / K * 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic",
         "config": {"workload": "fused residual add + RMSNorm fp16 [8192,2048] (configs[1])",
-                   "rows": rows, "hidden": hidden, "eps": wl.EPS, "accumulate": "f32",
-                   "input_sets": head["sets"], "algorithmic_bytes_per_step": nbytes},
+                   "rows": 8192, "hidden": 2048, "eps": b.wl.EPS, "accumulate": "f32",
+                   "input_sets": R, "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["GBps"] / PEAK_GBS, 4),
-                     "traffic": traffic.get("add_rmsnorm_8192x2048")},
+                     "traffic": b.traffic.get("add_rmsnorm_8192x2048")},
         "cpu_baseline": cpu,
-        "kernels": kernels,
+        "kernels": b.kernels,
     }
     print(json.dumps(rec), flush=True)
     return 0
-
-
-def bench_decode_step(llmk, wl, timer, torch, np, dev, K, W, n_seqs=256) -> dict:
-    import importlib
-    weights = importlib.import_module("llmk.weights")
-    cfg = llmk.ModelConfig()
-    lens = wl.attention_lens(n_seqs)
-    tokens, pos, tables, used = wl.decode_step_rows(lens)
-    n = lens.size
-    eng = llmk.Engine(cfg, max_rows=n, max_pages=128, num_pages=used)
-    w = weights.random_weights(cfg, wl.SEED_BASE + 9, device=dev)
-    eng.set_weights(*weights.engine_layers(w, cfg))
-    del w
-    g = torch.Generator(device=dev)
-    g.manual_seed(wl.SEED_BASE + 10)
-    fill = torch.randn(used * wl.PAGE * wl.N_KV * wl.HEAD_DIM, generator=g, device=dev).half()
-    for l in range(cfg.n_layers):
-        for which in (llmk.BUF_K_POOL, llmk.BUF_V_POOL):
-            eng.write_pool(which, l, fill)
-    del fill
-    torch.cuda.empty_cache()
-    eng.tune(n)     # time hipBLASLt's candidates for this batch's projection shapes
-    eng.set_rows(tokens, pos, tables)
-    eng.forward(n)  # eager once before capture
-    torch.cuda.synchronize()
-    if not torch.isfinite(eng.logits(n).float()).all():
-        raise RuntimeError("decode step produced non-finite logits")
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        eng.forward(n, stream=s)
-    torch.cuda.current_stream().wait_stream(s)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        eng.forward(n)
-    steps = max(20, K // 4)
-    t = timer.run(lambda i: graph.replay(), 1, steps, max(5, W // 4))
-    nbytes = wl.bytes_decode_step(lens)
-    path = ("fused few-rows projections (libllmk) with the norms, RoPE + scatter, SwiGLU and "
-            "residual adds inside them" if n <= llmk.LINEAR_ROWS_MAX else
-            "hipBLASLt projections + libllmk kernels")
-    e = kernel_entry(f"decode step 1B, {n} seqs (graph)", nbytes, t, None, {
-        "tokens_per_s": round(n / t["mean_s"], 1), "seqs": int(n),
-        "context_tokens": int(lens.sum()), "layers": cfg.n_layers,
-        "note": f"engine forward pass: {path}, one HIP graph; bytes = sum of the step's "
-                "kernels' algorithmic bytes (weights 2.47 GB, KV cache reads, activations "
-                "between kernels)"})
-    log(f"    -> {e['tokens_per_s']:.0f} tokens/s")
-    eng.close()
-    del graph
-    torch.cuda.empty_cache()
-    return {f"decode_step_1b_{n}": e}
-
-
-def bench_scheduler(llmk, wl, torch, np, dev) -> dict:
-    """The reference's scheduler benchmark on the engine (Llama-3.2-1B shape, seeded random
-    weights): 24 requests (prompts of 5 to 402 tokens, 32 new tokens each, one eligible every 2
-    iterations), 256 pages of 16, one request at a time and up to 8 at once, two rounds each as
-    the reference runs them (ref: tests/test_scheduler.cu:14-76). words/s = new tokens over the
-    scheduler's own wall clock (first iteration to last retirement), as the reference reports
-    it. Decode steps of each batch size run from the engine's HIP graph cache."""
-    import importlib
-    weights = importlib.import_module("llmk.weights")
-    cfg = llmk.ModelConfig()
-    max_len = max(wl.SCHED_PROMPT_LENS) + wl.SCHED_NEW
-    max_pages = (max_len + wl.PAGE - 1) // wl.PAGE
-    max_rows = 512  # the longest prompt (402 tokens) prefills in one pass
-    eng = llmk.Engine(cfg, max_rows=max_rows, max_pages=max_pages, num_pages=wl.SCHED_PAGES)
-    # A wide embedding (std 0.5) makes the logits peaked, so that the greedy tokens do not hinge
-    # on last-bit differences: a sequence's bits depend on its batch (the attention's split
-    # count follows the batch size), as cuBLAS results do in the reference.
-    w = weights.random_weights(cfg, wl.SEED_BASE + 9, device=dev, embed_std=0.5)
-    eng.set_weights(*weights.engine_layers(w, cfg))
-    del w
-    torch.cuda.empty_cache()
-    stream = torch.cuda.Stream()
-    model = eng.sched_model(stream)
-    reqs = wl.scheduler_requests()
-    order = np.random.default_rng(wl.SEED_BASE + 12).permutation(wl.SCHED_PAGES).astype(np.int32)
-
-    def run(rs, max_running):
-        pages = llmk.PageAllocator(wl.SCHED_PAGES)
-        pages.set_free_list(order)
-        outs, stats, _ = llmk.run_scheduler(rs, max_running, max_pages, wl.PAGE, pages, model)
-        if pages.num_free() != wl.SCHED_PAGES:
-            raise RuntimeError("scheduler run leaked pages")
-        return outs, stats
-
-    run(reqs[:2], wl.SCHED_MAX_RUNNING)  # warm-up, as the reference does
-    run(reqs[:wl.SCHED_MAX_RUNNING], wl.SCHED_MAX_RUNNING)  # captures the decode graphs
-    rounds = []
-    outputs = {}
-    for rnd in (1, 2):
-        for mr in (1, wl.SCHED_MAX_RUNNING):
-            outs, st = run(reqs, mr)
-            if mr in outputs and outputs[mr] != outs:
-                raise RuntimeError("scheduler outputs changed between rounds")
-            outputs[mr] = outs
-            wps = st["total_words"] / (st["total_ms"] * 1e-3)
-            rounds.append({"round": rnd, "max_running": mr, "decode_steps": st["decode_steps"],
-                           "mean_batch": round(st["mean_batch"], 2),
-                           "total_ms": round(st["total_ms"], 2),
-                           "prefill_ms": round(st["prefill_ms"], 2),
-                           "decode_ms": round(st["decode_ms"], 2),
-                           "words_per_s": round(wps, 1)})
-            log(f"  scheduler round {rnd}, up to {mr} at once: {st['decode_steps']} decode "
-                f"steps, mean batch {st['mean_batch']:.1f}, {st['total_ms']:.1f} ms, "
-                f"{wps:.0f} words/s")
-    if outputs[1] != outputs[wl.SCHED_MAX_RUNNING]:
-        raise RuntimeError("batched and one-at-a-time scheduler outputs differ")
-    best = {mr: max(r["words_per_s"] for r in rounds if r["max_running"] == mr)
-            for mr in (1, wl.SCHED_MAX_RUNNING)}
-    eng.close()
-    torch.cuda.empty_cache()
-    return {"scheduler_24x32_1b": {
-        "label": "continuous batching, 24 requests x 32 new tokens (Llama-3.2-1B shape)",
-        "words_per_s": best[wl.SCHED_MAX_RUNNING], "words_per_s_one_at_a_time": best[1],
-        "gain": round(best[wl.SCHED_MAX_RUNNING] / best[1], 2), "rounds": rounds,
-        "note": "reference on an RTX 4050 Laptop: 249 words/s up to 8 at once, 60 one at a "
-                "time (docs/scheduler_results.md); outputs identical in both modes"}}
-
-
-def cpu_baseline(inp, rows, hidden, nbytes, seconds, eps):
-    """Times the oracle's add_rmsnorm on host copies of the first input set: all usable cores
-    (threads split by rows), then one core, over a bounded number of full [8192, 2048] passes."""
-    import numpy as np
-    sys.path.insert(0, ROOT)
-    import oracle
-    oracle.lib()
-    r0 = inp["residual"].numpy().view(np.uint16).copy()
-    x = inp["x"].numpy().view(np.uint16)
-    w = inp["w"].numpy().view(np.uint16)
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-
-    def timed(nthreads, budget):
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            r = r0.copy()
-            oracle.add_rmsnorm(r, x, w, rows, hidden, eps, threads=nthreads)
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= budget:
-                return reps, el
-
-    reps, el = timed(threads, seconds * 0.7)
-    reps1, el1 = timed(1, seconds * 0.3)
-    v = nbytes * reps / el / 1e9
-    v1 = nbytes * reps1 / el1 / 1e9
-    log(f"  CPU oracle add_rmsnorm: {v:.2f} GB/s on {threads} threads, {v1:.2f} GB/s on 1")
-    return {"value": round(v, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} full [8192,2048] add_rmsnorm passes ({el:.1f} s) of the scalar C "
-                      f"oracle, rows split over {threads} threads",
-            "one_core": {"value": round(v1, 3), "unit": "GB/s", "cores": 1,
-                         "sample": f"{reps1} passes ({el1:.1f} s)"}}
 
 
 if __name__ == "__main__":

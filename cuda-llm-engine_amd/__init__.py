@@ -144,6 +144,8 @@ _SIGS = {
     "llmk_kv_scatter_batch": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "llmk_rope_kv_scatter_batch": (_i, [_vp] * 8 + [_i] * 6 + [_vp]),
     "llmk_copy_bytes": (_i, [_vp, _vp, _sz, _vp]),
+    "llmk_bw_probe": (_i, [_i, _vp, _vp, _vp, _sz, _i, _i, _vp]),
+    "llmk_empty_launch": (_i, [_i, _i, _vp]),
     "llmk_attention_decode_fast_workspace_floats": (_sz, [_i, _i, _i]),
     "llmk_argmax_rows": (_i, [_vp, _vp, _i, _i, _vp]),
     "llmk_attention_decode_fast": (_i, [_vp] * 7 + [_i] * 7 + [_vp]),
@@ -469,6 +471,31 @@ def copy_bytes(src, dst, nbytes: int, stream=None) -> None:
     if src.device.type != "cuda" or dst.device.type != "cuda":
         _fail(fn, "buffers must be CUDA tensors")
     _check(fn, _lib.llmk_copy_bytes(src.data_ptr(), dst.data_ptr(), nbytes, _stream(stream)))
+
+
+PROBE_READ, PROBE_COPY, PROBE_READ2, PROBE_INPLACE, PROBE_WRITE = range(5)
+
+
+def bw_probe(mode: int, dst, nbytes: int, a=None, b=None, blocks: int = 0, unroll: int = 4,
+             stream=None) -> None:
+    """Bandwidth probe of one traffic mix (``llmk_bw_probe``; PROBE_READ reads `a`, PROBE_COPY
+    a -> dst, PROBE_READ2 a, b -> dst, PROBE_INPLACE rewrites dst, PROBE_WRITE fills dst)."""
+    fn = "bw_probe"
+    for name, t in (("dst", dst), ("a", a), ("b", b)):
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            _fail(fn, f"{name} must be a CUDA tensor")
+        if t.numel() * t.element_size() < nbytes:
+            _fail(fn, f"{name} holds fewer than nbytes")
+    _check(fn, _lib.llmk_bw_probe(mode, None if a is None else a.data_ptr(),
+                                  None if b is None else b.data_ptr(), dst.data_ptr(), nbytes,
+                                  blocks, unroll, _stream(stream)))
+
+
+def empty_launch(blocks: int, threads: int, stream=None) -> None:
+    """An empty kernel of blocks x threads (``llmk_empty_launch``): the launch floor."""
+    _check("empty_launch", _lib.llmk_empty_launch(blocks, threads, _stream(stream)))
 
 
 class DecodeNonGemmPass:

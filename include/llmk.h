@@ -177,6 +177,27 @@ LLMK_API int llmk_argmax_rows(const uint16_t* logits, int32_t* out, int n_rows, 
  * nbytes % 16 == 0. ref: bench/bandwidth.cu:11-15 (copy_vec4, the reference's bandwidth probe). */
 LLMK_API int llmk_copy_bytes(const void* src, void* dst, size_t nbytes, void* stream);
 
+/* Bandwidth probe for one traffic mix, with the layer kernels' 16-byte non-temporal accesses:
+ * LLMK_PROBE_READ reads a (dst receives nothing in practice, but must hold nbytes), _COPY a ->
+ * dst, _READ2 a, b -> dst (2 reads : 1 write), _INPLACE dst -> dst (read and rewrite the same
+ * addresses), _WRITE fills dst. blocks > 0: a grid-stride loop over that many 256-thread
+ * blocks; blocks == 0: one pass, every thread `unroll` vectors. unroll is 1, 2, 4 or 8.
+ * Buffers 16-byte aligned, nbytes % 16 == 0. INPLACE and WRITE change dst's contents.
+ * ref: bench/bandwidth.cu:11-62 (a copy kernel swept over block and grid sizes). */
+#define LLMK_PROBE_READ 0
+#define LLMK_PROBE_COPY 1
+#define LLMK_PROBE_READ2 2
+#define LLMK_PROBE_INPLACE 3
+#define LLMK_PROBE_WRITE 4
+LLMK_API int llmk_bw_probe(int mode, const void* a, const void* b, void* dst, size_t nbytes,
+                           int blocks, int unroll, void* stream);
+
+/* Launches an empty kernel of `blocks` blocks of `threads` threads: the launch floor a
+ * sequence of launches pays whatever the kernels do (the reference times its stages one by one
+ * with events, bench/bench_breakdown.cu:18-26; this measures what is left when the work is
+ * gone). */
+LLMK_API int llmk_empty_launch(int blocks, int threads, void* stream);
+
 /* One non-GEMM decode-step pass: the embedding gather into `residual`, then per layer l the
  * operations the reference's batched layer issues between its GEMMs and attention
  * (ref: engine/batched.cu:51-71, :112-115): add+RMSNorm of residual with x[l] (out normed[l]),

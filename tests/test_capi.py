@@ -118,6 +118,17 @@ def test_argument_validation_without_launch(llmk):
     assert L.llmk_attention_decode_fast_workspace_floats(256, 32, 32) == 256 * 32 * 32 * 66
     assert L.llmk_attention_decode_fast_workspace_floats(0, 32, 32) == 0
     assert L.llmk_argmax_rows(None, None, 0, 128256, None) == 0
+    # measurement kernels
+    P = L.llmk_bw_probe
+    assert P(E.PROBE_COPY, None, None, None, 0, 0, 4, None) == 0
+    assert P(5, FAKE, FAKE, FAKE, 32, 0, 4, None) == E.LLMK_ERR_INVALID_VALUE
+    assert P(E.PROBE_READ2, FAKE, None, FAKE, 32, 0, 4, None) == E.LLMK_ERR_INVALID_VALUE
+    assert P(E.PROBE_COPY, FAKE, None, FAKE, 32, -1, 4, None) == E.LLMK_ERR_INVALID_VALUE
+    assert P(E.PROBE_COPY, FAKE, None, FAKE, 24, 0, 4, None) == E.LLMK_ERR_SHAPE
+    assert P(E.PROBE_INPLACE, None, None, MIS, 32, 0, 4, None) == E.LLMK_ERR_ALIGNMENT
+    assert P(E.PROBE_COPY, FAKE, None, FAKE, 32, 0, 3, None) == E.LLMK_ERR_INVALID_VALUE
+    assert L.llmk_empty_launch(0, 64, None) == E.LLMK_ERR_INVALID_VALUE
+    assert L.llmk_empty_launch(4, 2048, None) == E.LLMK_ERR_INVALID_VALUE
     assert L.llmk_argmax_rows(FAKE, FAKE, 4, 0, None) == E.LLMK_ERR_INVALID_VALUE
     assert L.llmk_argmax_rows(None, FAKE, 4, 100, None) == E.LLMK_ERR_INVALID_VALUE
 

@@ -567,7 +567,7 @@ def test_engine_rejects_a_pass_over_rows_not_uploaded(llmk):
     e.forward(3, 1)
     torch.cuda.synchronize()
     before = e.logits(1).view(torch.int16).clone()
-    e.set_rows([4, 5], [1, 2], [[0, 1], [2, 3]])
+    e.set_rows([4, 5], [0, 0], [[0, 1], [2, 3]])     # each row reads only its own position
     for n, nl in ((3, -1), (2, 1), (3, 1)):
         with pytest.raises(llmk.LlmkError) as ei:
             e.forward(n, nl)
