@@ -244,30 +244,63 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
                 line += f" algorithmic_bytes={alg} ratio={traffic / alg:.4f}"
         print(line)
     print("#")
-    print("# Every kernel of every section: calls, mean / min / max duration (us), grid")
-    print("# (work-items), kernel.")
+    print("# The libllmk and hipBLASLt kernels of every section (input generation and the timer's")
+    print("# spin kernel left out): calls, mean / min / max duration (us), grid (work-items), kernel.")
     sections = []
     for k in dur:
         if k[0] not in sections:
             sections.append(k[0])
     for sec in sections:
+        ks = [k for k in dur if k[0] == sec and _own_kernel(k[1])]
+        if not ks:
+            continue
         print(f"## section {sec}")
-        for k in sorted((k for k in dur if k[0] == sec), key=lambda k: -sum(dur[k])):
+        for k in sorted(ks, key=lambda k: -sum(dur[k])):
             d = dur[k]
             print(f"#   {len(d):6d} {sum(d) / len(d):9.3f} {min(d):9.3f} {max(d):9.3f} "
                   f"{k[2]:9d}  {k[1][:96]}")
-    # kernel time per pass: the pass graph's kernels over its number of passes (embeddings)
-    pk = [k for k in dur if k[0] == "pass_graph"]
-    passes = sum(len(dur[k]) for k in pk if "k_embedding" in k[1])
-    if passes:
-        total = sum(sum(dur[k]) for k in pk) / passes
-        print("#")
-        print(f"# pass_graph: {passes} passes, kernel time per pass {total:.2f} us "
-              f"(sum of the 49 kernels' durations; the event-timed pass includes the gaps)")
-        for k in sorted(pk, key=lambda k: -sum(dur[k])):
-            print(f"#   {len(dur[k]) / passes:6.2f} launches/pass x {sum(dur[k]) / len(dur[k]):7.3f}"
-                  f" us = {sum(dur[k]) / passes:7.2f} us/pass  {k[1][:80]}")
+    print("#")
+    summarize_pass(_by_section(_csv_rows(trace_dir, "kernel_trace.csv")))
     return 1 if missing else 0
+
+
+def _own_kernel(name: str) -> bool:
+    return "llmk" in name or name.startswith("Cijk")
+
+
+def summarize_pass(tagged):
+    """The 16-layer pass on the traced GPU timeline: each graph replay of the pass_graph
+    section is the 49 kernels from an embedding gather on. Its span (first start to last end)
+    is the pass as the GPU ran it under the profiler; the kernels' durations add up to the span
+    less the gaps between them."""
+    rows = [r for sec, r in tagged if sec == "pass_graph" and _own_kernel(r["Kernel_Name"])]
+    passes, cur = [], None
+    for r in rows:
+        if "k_embedding" in r["Kernel_Name"]:
+            cur = []
+            passes.append(cur)
+        if cur is not None:
+            cur.append(r)
+    passes = [p for p in passes if len(p) == 49]
+    if not passes:
+        print("# pass_graph: no complete passes found")
+        return
+    span = busy = 0.0
+    per_kernel = {}
+    for p in passes:
+        st = [int(r["Start_Timestamp"]) for r in p]
+        en = [int(r["End_Timestamp"]) for r in p]
+        span += (max(en) - min(st)) * 1e-3
+        for r in p:
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+            busy += d
+            per_kernel.setdefault(r["Kernel_Name"], []).append(d)
+    n = len(passes)
+    print(f"# pass_graph: {n} passes of 49 kernels on the traced timeline: span {span / n:.2f} us "
+          f"per pass = kernel durations {busy / n:.2f} us + gaps {(span - busy) / n:.2f} us")
+    for name, d in sorted(per_kernel.items(), key=lambda kv: -sum(kv[1])):
+        print(f"#   {len(d) / n:6.2f} launches/pass x {sum(d) / len(d):7.3f} us = "
+              f"{sum(d) / n:7.2f} us/pass  {name[:80]}")
 
 
 def summarize_step(trace_dir, n_rows=256):
