@@ -33,6 +33,7 @@ LLMK_ERR_UNSUPPORTED = 10004
 LLMK_ERR_BLAS = 10005
 LLMK_ERR_IO = 10006
 LLMK_ERR_CAPACITY = 10007
+LLMK_ERR_SCRATCH = 10008
 
 
 class LlmkError(RuntimeError):
@@ -149,6 +150,7 @@ _SIGS = {
     "llmk_attention_decode_fast_workspace_floats": (_sz, [_i, _i, _i]),
     "llmk_argmax_rows": (_i, [_vp, _vp, _i, _i, _vp]),
     "llmk_attention_decode_fast": (_i, [_vp] * 7 + [_i] * 7 + [_vp]),
+    "llmk_attention_decode_fast_noalloc": (_i, [_vp] * 6 + [_i] * 7 + [_vp]),
     "llmk_decode_nongemm_pass": (_i, [ctypes.POINTER(DecodePass), _vp]),
     "llmk_blas_create": (_i, [ctypes.POINTER(_vp)]),
     "llmk_blas_destroy": (None, [_vp]),
@@ -400,6 +402,8 @@ def rope_kv_scatter_batch(q, k, v, k_pool, v_pool, block_tables, positions, inv_
 
 # Default of choose_num_splits; the same value as LLMK_ATTN_TARGET_BLOCKS in include/llmk.h.
 ATTN_TARGET_BLOCKS = 65536
+# Scratch floats of llmk_attention_decode_fast_noalloc (LLMK_ATTN_NOALLOC_MAX_FLOATS).
+ATTN_NOALLOC_MAX_FLOATS = 256 * 32 * 32 * 66
 
 
 def choose_num_splits(n_seq: int, n_kv_heads: int, max_seq_len: int,

@@ -26,6 +26,8 @@
 // (A, m, l) in the workspace and a second kernel merges the splits.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.hpp"
 
 namespace llmk {
@@ -872,12 +874,11 @@ extern "C" size_t llmk_attention_decode_fast_workspace_floats(int n_seq, int n_h
   return (size_t)n_seq * n_heads * num_splits * (kHeadDim + 2);
 }
 
-extern "C" int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_pool,
-                                          const uint16_t* v_pool, const int32_t* block_tables,
-                                          const int32_t* seq_lens, uint16_t* out,
-                                          float* workspace, int n_seq, int max_pages,
-                                          int page_size, int n_heads, int n_kv_heads,
-                                          int head_dim, int num_splits, void* stream) {
+// Argument checks shared by both entry points; -1 means "go ahead".
+static int check_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                           const int32_t* block_tables, const int32_t* seq_lens,
+                           const uint16_t* out, int n_seq, int max_pages, int page_size,
+                           int n_heads, int n_kv_heads, int head_dim, int num_splits) {
   if (n_seq == 0) return LLMK_OK;
   // The reference's preconditions (kernels/attention_decode_fast.cu:160-163).
   if (page_size != kPage || head_dim != kHeadDim || n_kv_heads <= 0 ||
@@ -887,10 +888,15 @@ extern "C" int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_p
   if (n_seq > 65535 || n_kv_heads / 8 > 65535) return LLMK_ERR_UNSUPPORTED;
   if (!q || !k_pool || !v_pool || !block_tables || !seq_lens || !out)
     return LLMK_ERR_INVALID_VALUE;
-  if (num_splits > 1 && !workspace) return LLMK_ERR_INVALID_VALUE;
-  if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out) ||
-      (workspace && !aligned16(workspace)))
+  if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
     return LLMK_ERR_ALIGNMENT;
+  return -1;
+}
+
+static int run_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                         const int32_t* block_tables, const int32_t* seq_lens, uint16_t* out,
+                         float* workspace, int n_seq, int max_pages, int n_heads, int n_kv_heads,
+                         int num_splits, void* stream) {
   AttnArgs a;
   a.q = reinterpret_cast<const f16*>(q);
   a.k_pool = reinterpret_cast<const f16*>(k_pool);
@@ -915,4 +921,76 @@ extern "C" int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_p
     case 1: return attn_launch<1>(a, s);
     default: return LLMK_ERR_UNSUPPORTED;  // a row of 3, 5, 6 or 7 kv heads
   }
+}
+
+extern "C" int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_pool,
+                                          const uint16_t* v_pool, const int32_t* block_tables,
+                                          const int32_t* seq_lens, uint16_t* out,
+                                          float* workspace, int n_seq, int max_pages,
+                                          int page_size, int n_heads, int n_kv_heads,
+                                          int head_dim, int num_splits, void* stream) {
+  const int st = check_attention(q, k_pool, v_pool, block_tables, seq_lens, out, n_seq,
+                                 max_pages, page_size, n_heads, n_kv_heads, head_dim,
+                                 num_splits);
+  if (st != -1) return st;
+  if (num_splits > 1 && !workspace) return LLMK_ERR_INVALID_VALUE;
+  if (workspace && !aligned16(workspace)) return LLMK_ERR_ALIGNMENT;
+  return run_attention(q, k_pool, v_pool, block_tables, seq_lens, out, workspace, n_seq,
+                       max_pages, n_heads, n_kv_heads, num_splits, stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Allocation-free variant: the per-piece partials go to `scratch`, a file-scope device array
+// (each GPU the library runs on holds its own copy until the process ends), instead of a
+// caller workspace. Its size is the workspace of 256 sequences x 32 query heads x 32 splits,
+// 66 MiB. Host code never passes the array's name to a kernel or a copy: the name is a host
+// stand-in, and its device address is resolved once per device (with that device current) by
+// hipGetSymbolAddress and kept in scratch_dev[]. All calls on one GPU share its array, so
+// calls that overlap on one GPU (different streams, no ordering between them) race. Nothing
+// in it needs clearing: every call writes each partial it reads, and the piece count, first.
+// ---------------------------------------------------------------------------------------------
+constexpr size_t kScratchFloats = (size_t)256 * 32 * 32 * (kHeadDim + 2);
+static_assert(kScratchFloats == LLMK_ATTN_NOALLOC_MAX_FLOATS, "llmk.h states the scratch size");
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+static float* scratch_dev[kMaxDevices];
+static std::mutex scratch_mu;
+
+// The current device's address of `scratch`, resolved on the first call on that device.
+static int scratch_address(float** out) {
+  int dev = 0;
+  int st = (int)hipGetDevice(&dev);
+  if (st != LLMK_OK) return st;
+  if (dev < 0 || dev >= kMaxDevices) return LLMK_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    st = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (st != LLMK_OK) return st;
+    if (!p) return LLMK_ERR_INVALID_VALUE;
+    scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *out = scratch_dev[dev];
+  return LLMK_OK;
+}
+
+extern "C" int llmk_attention_decode_fast_noalloc(const uint16_t* q, const uint16_t* k_pool,
+                                                  const uint16_t* v_pool,
+                                                  const int32_t* block_tables,
+                                                  const int32_t* seq_lens, uint16_t* out,
+                                                  int n_seq, int max_pages, int page_size,
+                                                  int n_heads, int n_kv_heads, int head_dim,
+                                                  int num_splits, void* stream) {
+  const int st = check_attention(q, k_pool, v_pool, block_tables, seq_lens, out, n_seq,
+                                 max_pages, page_size, n_heads, n_kv_heads, head_dim,
+                                 num_splits);
+  if (st != -1) return st;
+  const size_t need = llmk_attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits);
+  if (need > kScratchFloats) return LLMK_ERR_SCRATCH;
+  float* ws = nullptr;
+  const int sa = scratch_address(&ws);
+  if (sa != LLMK_OK) return sa;
+  return run_attention(q, k_pool, v_pool, block_tables, seq_lens, out, ws, n_seq, max_pages,
+                       n_heads, n_kv_heads, num_splits, stream);
 }

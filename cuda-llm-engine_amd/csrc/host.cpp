@@ -15,6 +15,8 @@ extern "C" const char* llmk_error_string(int status) {
     case LLMK_ERR_BLAS: return "llmk: hipBLASLt could not run the GEMM";
     case LLMK_ERR_IO: return "llmk: weight file missing, short, or without a required tensor";
     case LLMK_ERR_CAPACITY: return "llmk: a request can never fit in the page pool or block table";
+    case LLMK_ERR_SCRATCH:
+      return "llmk: the call needs more scratch than the allocation-free entry point holds";
     default: return hipGetErrorString(static_cast<hipError_t>(status));
   }
 }

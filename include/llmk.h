@@ -44,6 +44,7 @@ extern "C" {
 #define LLMK_ERR_BLAS 10005          /* hipBLASLt refused or failed a GEMM */
 #define LLMK_ERR_IO 10006            /* a weight file is missing, short, or lacks a tensor */
 #define LLMK_ERR_CAPACITY 10007      /* a request can never fit in the page pool or block table */
+#define LLMK_ERR_SCRATCH 10008       /* more scratch than the allocation-free entry point holds */
 
 /* Human-readable name of a status code (LLMK_ERR_* or hipError_t). Never NULL. */
 LLMK_API const char* llmk_error_string(int status);
@@ -163,6 +164,28 @@ LLMK_API int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_poo
                                         float* workspace, int n_seq, int max_pages,
                                         int page_size, int n_heads, int n_kv_heads,
                                         int head_dim, int num_splits, void* stream);
+
+/* Scratch floats of llmk_attention_decode_fast_noalloc: the workspace of 256 sequences x 32
+ * query heads x 32 splits (66 MiB per GPU, held from the library's load to the process's end). */
+#define LLMK_ATTN_NOALLOC_MAX_FLOATS ((size_t)256 * 32 * 32 * 66)
+
+/* llmk_attention_decode_fast without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The same kernels and results as
+ * llmk_attention_decode_fast; the partial results go to a device array inside the library
+ * instead, one per GPU. Returns LLMK_ERR_SCRATCH, before any launch, when
+ * llmk_attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits) exceeds
+ * LLMK_ATTN_NOALLOC_MAX_FLOATS. Calls no allocating routine. All calls on one GPU share that
+ * GPU's array: calls that may overlap on one GPU (unordered streams) race, and must be ordered
+ * by the caller. The first call on a device also resolves the array's device address there
+ * (hipGetSymbolAddress, not a stream operation). */
+LLMK_API int llmk_attention_decode_fast_noalloc(const uint16_t* q, const uint16_t* k_pool,
+                                                const uint16_t* v_pool,
+                                                const int32_t* block_tables,
+                                                const int32_t* seq_lens, uint16_t* out, int n_seq,
+                                                int max_pages, int page_size, int n_heads,
+                                                int n_kv_heads, int head_dim, int num_splits,
+                                                void* stream);
 
 /* Row argmax of fp16 logits [n_rows, vocab]: out[r] = the index of the largest value of row r,
  * the lowest index among equal values (+0 equals -0); NaN is never chosen; a row with no value

@@ -116,6 +116,15 @@ def test_argument_validation_without_launch(llmk):
     assert A(*[FAKE] * 6, None, 4, 8, 16, 32, 8, 64, 2, None) == E.LLMK_ERR_INVALID_VALUE
     assert A(MIS, *[FAKE] * 6, 4, 8, 16, 32, 8, 64, 2, None) == E.LLMK_ERR_ALIGNMENT
     assert L.llmk_attention_decode_fast_workspace_floats(256, 32, 32) == 256 * 32 * 32 * 66
+    # the allocation-free variant: same checks, and a batch past its scratch is refused
+    N = L.llmk_attention_decode_fast_noalloc
+    assert N(None, None, None, None, None, None, 0, 8, 16, 32, 8, 64, 4, None) == 0
+    assert N(*[FAKE] * 6, 4, 8, 32, 32, 8, 64, 4, None) == E.LLMK_ERR_SHAPE
+    assert N(*[FAKE] * 5, None, 4, 8, 16, 32, 8, 64, 4, None) == E.LLMK_ERR_INVALID_VALUE
+    assert N(MIS, *[FAKE] * 5, 4, 8, 16, 32, 8, 64, 2, None) == E.LLMK_ERR_ALIGNMENT
+    assert N(*[FAKE] * 6, 257, 8, 16, 32, 8, 64, 32, None) == E.LLMK_ERR_SCRATCH
+    assert N(*[FAKE] * 6, 3, 8, 16, 4096, 1024, 64, 32, None) == E.LLMK_ERR_SCRATCH
+    assert E.ATTN_NOALLOC_MAX_FLOATS == L.llmk_attention_decode_fast_workspace_floats(256, 32, 32)
     assert L.llmk_attention_decode_fast_workspace_floats(0, 32, 32) == 0
     assert L.llmk_argmax_rows(None, None, 0, 128256, None) == 0
     # measurement kernels
