@@ -260,8 +260,46 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
             print(f"#   {len(d):6d} {sum(d) / len(d):9.3f} {min(d):9.3f} {max(d):9.3f} "
                   f"{k[2]:9d}  {k[1][:96]}")
     print("#")
-    summarize_pass(_by_section(_csv_rows(trace_dir, "kernel_trace.csv")))
+    tagged = _by_section(_csv_rows(trace_dir, "kernel_trace.csv"))
+    summarize_spread(tagged)
+    print("#")
+    summarize_pass(tagged)
     return 1 if missing else 0
+
+
+def summarize_spread(tagged):
+    """Duration spread of each configuration kernel in its section, by what precedes the
+    launch on the GPU: back to back (the previous kernel ended < 1 us before it started), after
+    a short gap (1-20 us: the host's enqueue or an event), or after idle (> 20 us: a
+    synchronisation, between timing passes). Quantiles in us."""
+    import statistics
+    print("# Duration spread of the configuration kernels by the gap in front of each launch")
+    print("# (back to back: < 1 us after the previous kernel's end; gap: 1-20 us; idle: > 20 us):")
+    print("#   label  class  launches  mean  p1  p10  p50  p90  p99  max")
+    by_sec = {}
+    order = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), sec, r["Kernel_Name"],
+                    _grid(r)) for sec, r in tagged)
+    prev_end = None
+    for st, en, sec, name, g in order:
+        gap = None if prev_end is None else (st - prev_end) * 1e-3
+        prev_end = en if prev_end is None else max(prev_end, en)
+        by_sec.setdefault((sec, name, g), []).append(((en - st) * 1e-3, gap))
+    for label, sec, name, g, alg in PROFILE_SHAPES:
+        if sec.startswith("pass") or "merge" in label:
+            continue
+        keys = [k for k in by_sec if k[0] == sec and name in k[1] and k[2] == g]
+        if not keys:
+            continue
+        rows = by_sec[keys[0]]
+        for cls, test in (("b2b", lambda x: x is not None and x < 1.0),
+                          ("gap", lambda x: x is not None and 1.0 <= x <= 20.0),
+                          ("idle", lambda x: x is None or x > 20.0)):
+            d = sorted(v for v, gp in rows if test(gp))
+            if not d:
+                continue
+            q = lambda f: d[min(len(d) - 1, int(f * len(d)))]
+            print(f"#   {label:26s} {cls:4s} {len(d):6d} {statistics.fmean(d):7.3f} {q(0.01):7.3f} "
+                  f"{q(0.1):7.3f} {q(0.5):7.3f} {q(0.9):7.3f} {q(0.99):7.3f} {d[-1]:7.3f}")
 
 
 def _own_kernel(name: str) -> bool:
