@@ -53,7 +53,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "llmk_kernels_bench_configs.txt")
 # Marker launches: llmk_empty_launch(MARK_BASE + index, 64) before each measurement.
 MARK_BASE = 50000
 SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_8192",
-            "pass_graph", "pass_eager", "pass_floor", "pass_stage_embedding",
+            "pass_graph", "pass_eager", "pass_layers", "pass_floor", "pass_stage_embedding",
             "pass_stage_add_rmsnorm", "pass_stage_rope_kv_scatter", "pass_stage_swiglu",
             "pass_floor_stages", "attention_256", "attention_16x2048", "attention_sweep",
             "argmax", "step_256", "step_8", "sched", "probe_sweep", "probe_kernels", "copy_1GiB",
@@ -63,10 +63,10 @@ SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_819
 # grid rules: the embedding and add+RMSNorm take one 64-thread wave per row below 4096 rows
 # (gather_scatter.hip rows_grid, norm.hip rmsnorm_launch); the fused RoPE + scatter one token
 # per 256-thread block below 2048 tokens (rope.hip tokens_per_block: 48 vectors of 16 B per
-# token, 2 per thread); SwiGLU 512 vectors per 256-thread block (swiglu.hip, UNROLL 2) over
-# 256 x 8192 values.
+# token, 2 per thread); SwiGLU one 16-byte vector of each input per lane in one-wave blocks
+# (swiglu.hip) over 256 x 8192 values.
 PASS_SHAPES = {"embedding": (256, 64), "add_rmsnorm": (256, 64),
-               "rope_kv_scatter": (256, 256), "swiglu": (512, 256)}
+               "rope_kv_scatter": (256, 256), "swiglu": (4096, 64)}
 
 
 def log(msg: str) -> None:
@@ -132,7 +132,7 @@ PROFILE_SHAPES = [
     ("rmsnorm_16x2048", "rmsnorm_16", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
     # 8 tokens per block, 10 vector tasks per thread (40 heads x 8 vectors x 8 tokens / 256)
     ("rope_8192", "rope_8192", "k_rope_vec", 1024 * 256, 83918976),
-    ("swiglu_8192x8192", "swiglu_8192", "k_swiglu_vecILi2E", 16384 * 256, 402653184),
+    ("swiglu_8192x8192", "swiglu_8192", "k_swiglu_vecILi1E", 131072 * 64, 402653184),
     ("embedding_8192", "embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
     ("copy_1GiB", "copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),
     # 512 blocks: two resident blocks of 256 threads on each of the 256 CUs (191 VGPRs).
@@ -149,7 +149,10 @@ PROFILE_SHAPES = [
      4198400),
     ("decode:rope_kv_scatter_256", "pass_graph", "k_rope_vecILi4ELi2ELb1ELb0E", 256 * 256,
      3147904),
-    ("decode:swiglu_256x8192", "pass_graph", "k_swiglu_vecILi2E", 512 * 256, 12582912),
+    ("decode:swiglu_256x8192", "pass_graph", "k_swiglu_vecILi1E", 4096 * 64, 12582912),
+    # the pass with one launch per layer: 256 norm rows, 256 RoPE tokens, 4096 SwiGLU chunks
+    ("decode_layers:layer_256", "pass_layers", "k_layer_passILi4ELb0ELi6E", 4608 * 64,
+     4198400 + 3147904 + 12582912),
 ]
 
 
@@ -263,7 +266,8 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
     tagged = _by_section(_csv_rows(trace_dir, "kernel_trace.csv"))
     summarize_spread(tagged)
     print("#")
-    summarize_pass(tagged)
+    summarize_pass(tagged, "pass_graph", "k_embedding", 49)
+    summarize_pass(tagged, "pass_layers", "k_layer_passILi4ELb1E", 16)
     return 1 if missing else 0
 
 
@@ -306,22 +310,22 @@ def _own_kernel(name: str) -> bool:
     return "llmk" in name or name.startswith("Cijk")
 
 
-def summarize_pass(tagged):
-    """The 16-layer pass on the traced GPU timeline: each graph replay of the pass_graph
-    section is the 49 kernels from an embedding gather on. Its span (first start to last end)
-    is the pass as the GPU ran it under the profiler; the kernels' durations add up to the span
-    less the gaps between them."""
-    rows = [r for sec, r in tagged if sec == "pass_graph" and _own_kernel(r["Kernel_Name"])]
+def summarize_pass(tagged, section, first, launches):
+    """The 16-layer pass on the traced GPU timeline: each graph replay of the section is
+    `launches` kernels from one whose name contains `first` on. Its span (first start to last
+    end) is the pass as the GPU ran it under the profiler; the kernels' durations add up to the
+    span less the gaps between them."""
+    rows = [r for sec, r in tagged if sec == section and _own_kernel(r["Kernel_Name"])]
     passes, cur = [], None
     for r in rows:
-        if "k_embedding" in r["Kernel_Name"]:
+        if first in r["Kernel_Name"]:
             cur = []
             passes.append(cur)
         if cur is not None:
             cur.append(r)
-    passes = [p for p in passes if len(p) == 49]
+    passes = [p for p in passes if len(p) == launches]
     if not passes:
-        print("# pass_graph: no complete passes found")
+        print(f"# {section}: no complete passes found")
         return
     span = busy = 0.0
     per_kernel = {}
@@ -334,8 +338,9 @@ def summarize_pass(tagged):
             busy += d
             per_kernel.setdefault(r["Kernel_Name"], []).append(d)
     n = len(passes)
-    print(f"# pass_graph: {n} passes of 49 kernels on the traced timeline: span {span / n:.2f} us "
-          f"per pass = kernel durations {busy / n:.2f} us + gaps {(span - busy) / n:.2f} us")
+    print(f"# {section}: {n} passes of {launches} kernels on the traced timeline: span "
+          f"{span / n:.2f} us per pass = kernel durations {busy / n:.2f} us + gaps "
+          f"{(span - busy) / n:.2f} us")
     for name, d in sorted(per_kernel.items(), key=lambda kv: -sum(kv[1])):
         print(f"#   {len(d) / n:6.2f} launches/pass x {sum(d) / len(d):7.3f} us = "
               f"{sum(d) / n:7.2f} us/pass  {name[:80]}")
@@ -685,6 +690,21 @@ class Bench:
         t = self.run(lambda i: dps[i].run(), 2, steps, warm)
         self.kernels["decode_pass_16x256_eager"] = kernel_entry(
             "decode pass 16 layers x 256 (eager)", nb, t, None, {"sets": 2})
+        # the same pass with one launch per layer (llmk_decode_nongemm_pass_layers), possible
+        # because the pass's per-layer inputs are independent; graphs of its 16 launches
+        lgraphs = [capture(dp.run_layers) for dp in dps]
+        self.mark("pass_layers")
+        t = self.run(lambda i: lgraphs[i].replay(), 2, steps, warm)
+        self.kernels["decode_pass_16x256_layers"] = kernel_entry(
+            "decode pass, one launch per layer (graph)", nb, t, None,
+            {"launches": L, "layers": L, "seqs": n, "sets": 2,
+             "note": "each layer's add+RMSNorm rows, RoPE + K/V scatter tokens and SwiGLU "
+                     "chunks as blocks of one launch, the embedding gather fused into the first "
+                     "residual add (bytes counted as for the 49-launch pass, which also writes "
+                     "and re-reads the 1 MB of embedding rows); valid for this pass, whose "
+                     "per-layer inputs are independent, not for a decode step with GEMMs "
+                     "between the ops"})
+        del lgraphs
 
         # ---- breakdown
         def stage_fn(op, p):

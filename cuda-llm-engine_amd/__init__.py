@@ -152,6 +152,7 @@ _SIGS = {
     "llmk_attention_decode_fast": (_i, [_vp] * 7 + [_i] * 7 + [_vp]),
     "llmk_attention_decode_fast_noalloc": (_i, [_vp] * 6 + [_i] * 7 + [_vp]),
     "llmk_decode_nongemm_pass": (_i, [ctypes.POINTER(DecodePass), _vp]),
+    "llmk_decode_nongemm_pass_layers": (_i, [ctypes.POINTER(DecodePass), _vp]),
     "llmk_blas_create": (_i, [ctypes.POINTER(_vp)]),
     "llmk_blas_destroy": (None, [_vp]),
     "llmk_linear": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
@@ -553,6 +554,11 @@ class DecodeNonGemmPass:
     def run(self, stream=None) -> None:
         _check("decode_nongemm_pass",
                _lib.llmk_decode_nongemm_pass(ctypes.byref(self._desc), _stream(stream)))
+
+    def run_layers(self, stream=None) -> None:
+        """The same pass with one launch per layer (``llmk_decode_nongemm_pass_layers``)."""
+        _check("decode_nongemm_pass_layers",
+               _lib.llmk_decode_nongemm_pass_layers(ctypes.byref(self._desc), _stream(stream)))
 
 
 # ---------------------------------------------------------------------------------------------

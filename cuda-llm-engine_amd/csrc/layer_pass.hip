@@ -1,0 +1,164 @@
+// The non-GEMM decode pass with one launch per layer (llmk_decode_nongemm_pass_layers).
+//
+// llmk_decode_nongemm_pass runs each op of a layer as its own launch (49 launches for 16
+// layers), the way a decode step with its GEMMs in between must. In the non-GEMM pass by itself
+// (config 5) a layer's add + RMSNorm, RoPE + K/V scatter and SwiGLU read independent inputs;
+// only the residual carries from one layer's norm to the next. So each layer here is ONE launch
+// of one-wave blocks: blocks [0, n) take the add + RMSNorm rows, blocks [n, 2n) the RoPE + K/V
+// scatter of one token each, the rest the SwiGLU chunks. The first layer's norm rows read their
+// residual input straight from the embedding table (the gather fused into the add), so the
+// pass is n_layers launches. Every block runs the same body as the stand-alone kernel
+// (layer_ops.hpp), so the results are the same bits. Blocks are dispatched in index order: the
+// latency-bound norm and RoPE blocks go first, the SwiGLU stream fills the rest.
+#include "layer_ops.hpp"
+
+namespace llmk {
+namespace {
+
+struct LayerArgs {
+  const f16 *x, *norm_w;
+  f16* normed;
+  f16* q;
+  const f16 *k, *v;
+  f16 *k_pool, *v_pool;
+  const f16 *gate, *up;
+  f16* act;
+  f16* residual;
+  const f16* embed;  // the embedding table (first layer only)
+  const int* ids;
+  const int *tables, *pos;
+  const float* inv_freq;
+  FastDiv qdiv, kdiv;
+  size_t swiglu_nvec;
+  int n, vpr, max_pages, page_size, nh, nkv;
+  float hidden_f, eps;
+};
+
+constexpr int kWave = 64;
+
+template <int VPL, bool EMBED, int TASKS>
+__global__ void __launch_bounds__(kWave) k_layer_pass(LayerArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int b = blockIdx.x;
+  if (b < a.n) {
+    const size_t base = (size_t)b * a.vpr * 8;
+    const f16* r_in = EMBED ? a.embed + (size_t)a.ids[b] * a.vpr * 8 : a.residual + base;
+    rmsnorm_row<VPL, true, true>(a.x + base, r_in, a.residual + base, a.norm_w, a.normed + base,
+                                 a.vpr, a.hidden_f, a.eps, threadIdx.x);
+  } else if (b < 2 * a.n) {
+    rope_tile<4, TASKS, true, false>(b - a.n, kWave, smem, a.q, a.k, a.v, a.k_pool, a.v_pool,
+                                     a.tables, a.pos, a.inv_freq, a.n, a.nh, a.nkv, 1,
+                                     a.max_pages, a.page_size, a.qdiv, a.kdiv, nullptr, 0);
+  } else {
+    constexpr size_t chunk = (size_t)kSwigluThreads * kSwigluUnroll;
+    static_assert(kSwigluThreads == kWave, "SwiGLU chunks are one-wave blocks");
+    const size_t cb = (size_t)(b - 2 * a.n) * chunk;
+    if (cb + chunk <= a.swiglu_nvec)
+      swiglu_block<kSwigluUnroll>(a.gate, a.up, a.act, cb, a.swiglu_nvec, true);
+    else
+      swiglu_block<kSwigluUnroll>(a.gate, a.up, a.act, cb, a.swiglu_nvec, false);
+  }
+}
+
+template <int VPL, bool EMBED>
+int launch_layer(const LayerArgs& a, int tasks, unsigned blocks, size_t lds, hipStream_t s) {
+  switch (tasks) {
+    case 6: return launch(k_layer_pass<VPL, EMBED, 6>, dim3(blocks), dim3(kWave), lds, s, a);
+    case 8: return launch(k_layer_pass<VPL, EMBED, 8>, dim3(blocks), dim3(kWave), lds, s, a);
+    case 12: return launch(k_layer_pass<VPL, EMBED, 12>, dim3(blocks), dim3(kWave), lds, s, a);
+    default: return launch(k_layer_pass<VPL, EMBED, 16>, dim3(blocks), dim3(kWave), lds, s, a);
+  }
+}
+
+template <bool EMBED>
+int launch_layer_vpl(const LayerArgs& a, int tasks, unsigned blocks, size_t lds, hipStream_t s) {
+  switch (a.vpr / 64) {
+    case 1: return launch_layer<1, EMBED>(a, tasks, blocks, lds, s);
+    case 2: return launch_layer<2, EMBED>(a, tasks, blocks, lds, s);
+    case 4: return launch_layer<4, EMBED>(a, tasks, blocks, lds, s);
+    case 8: return launch_layer<8, EMBED>(a, tasks, blocks, lds, s);
+    default: return launch_layer<16, EMBED>(a, tasks, blocks, lds, s);
+  }
+}
+
+}  // namespace
+}  // namespace llmk
+
+using namespace llmk;
+
+extern "C" int llmk_decode_nongemm_pass_layers(const llmk_decode_pass* p, void* stream) {
+  if (!p) return LLMK_ERR_INVALID_VALUE;
+  if (p->n_seqs < 0 || p->n_layers < 0 || p->hidden <= 0 || p->inter <= 0 ||
+      p->max_pages <= 0 || p->page_size <= 0 || p->n_heads < 0 || p->n_kv_heads <= 0)
+    return LLMK_ERR_INVALID_VALUE;
+  if (p->n_seqs == 0) return LLMK_OK;
+  if (!p->embed_table || !p->token_ids || !p->residual) return LLMK_ERR_INVALID_VALUE;
+  if (p->n_layers == 0)  // the embedding alone
+    return llmk_embedding_lookup(p->embed_table, p->token_ids, p->residual, p->n_seqs,
+                                 p->hidden, stream);
+  if (!p->x || !p->norm_w || !p->normed || !p->q || !p->k || !p->v || !p->k_pool ||
+      !p->v_pool || !p->gate || !p->up || !p->act || !p->block_tables || !p->positions ||
+      !p->inv_freq)
+    return LLMK_ERR_INVALID_VALUE;
+  // Shapes this launch implements; others take llmk_decode_nongemm_pass.
+  const int per_tok = (p->n_heads + 2 * p->n_kv_heads) * 8;  // 16-byte vectors per token
+  const int tasks = (per_tok + kWave - 1) / kWave;
+  const int vpl = p->hidden / 512;
+  if (p->head_dim != 64 || p->hidden % 512 != 0 || (vpl & (vpl - 1)) != 0 || vpl > 16 ||
+      p->inter % 8 != 0 || tasks > 16)
+    return LLMK_ERR_UNSUPPORTED;
+  const int ptasks = tasks <= 6 ? 6 : tasks <= 8 ? 8 : tasks <= 12 ? 12 : 16;
+  const int n = p->n_seqs;
+  auto al = [](const void* q) { return aligned16(q); };
+  if (!al(p->embed_table) || !al(p->residual)) return LLMK_ERR_ALIGNMENT;
+  for (int l = 0; l < p->n_layers; ++l) {
+    if (!p->x[l] || !p->norm_w[l] || !p->normed[l] || !p->q[l] || !p->k[l] || !p->v[l] ||
+        !p->k_pool[l] || !p->v_pool[l] || !p->gate[l] || !p->up[l] || !p->act[l])
+      return LLMK_ERR_INVALID_VALUE;
+    if (!al(p->x[l]) || !al(p->norm_w[l]) || !al(p->normed[l]) || !al(p->q[l]) ||
+        !al(p->k[l]) || !al(p->v[l]) || !al(p->k_pool[l]) || !al(p->v_pool[l]) ||
+        !al(p->gate[l]) || !al(p->up[l]) || !al(p->act[l]))
+      return LLMK_ERR_ALIGNMENT;
+  }
+  LayerArgs a;
+  a.residual = reinterpret_cast<f16*>(p->residual);
+  a.embed = reinterpret_cast<const f16*>(p->embed_table);
+  a.ids = p->token_ids;
+  a.tables = p->block_tables;
+  a.pos = p->positions;
+  a.inv_freq = p->inv_freq;
+  a.qdiv = make_fastdiv((uint32_t)(p->n_heads > 0 ? p->n_heads * 8 : 1));
+  a.kdiv = make_fastdiv((uint32_t)(p->n_kv_heads * 8));
+  a.swiglu_nvec = (size_t)n * p->inter / 8;
+  a.n = n;
+  a.vpr = p->hidden / 8;
+  a.max_pages = p->max_pages;
+  a.page_size = p->page_size;
+  a.nh = p->n_heads;
+  a.nkv = p->n_kv_heads;
+  a.hidden_f = (float)p->hidden;
+  a.eps = p->eps;
+  const size_t chunks = (a.swiglu_nvec + kSwigluThreads * kSwigluUnroll - 1) /
+                        (kSwigluThreads * kSwigluUnroll);
+  if (2 * (size_t)n + chunks > 0x7FFFFFFFu) return LLMK_ERR_UNSUPPORTED;
+  const unsigned blocks = (unsigned)(2 * (size_t)n + chunks);
+  const size_t lds = 8 + 64 * sizeof(f16);  // one token: its pool row, its (cos, sin) pairs
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int l = 0; l < p->n_layers; ++l) {
+    a.x = reinterpret_cast<const f16*>(p->x[l]);
+    a.norm_w = reinterpret_cast<const f16*>(p->norm_w[l]);
+    a.normed = reinterpret_cast<f16*>(p->normed[l]);
+    a.q = reinterpret_cast<f16*>(p->q[l]);
+    a.k = reinterpret_cast<const f16*>(p->k[l]);
+    a.v = reinterpret_cast<const f16*>(p->v[l]);
+    a.k_pool = reinterpret_cast<f16*>(p->k_pool[l]);
+    a.v_pool = reinterpret_cast<f16*>(p->v_pool[l]);
+    a.gate = reinterpret_cast<const f16*>(p->gate[l]);
+    a.up = reinterpret_cast<const f16*>(p->up[l]);
+    a.act = reinterpret_cast<f16*>(p->act[l]);
+    const int st = l == 0 ? launch_layer_vpl<true>(a, ptasks, blocks, lds, s)
+                          : launch_layer_vpl<false>(a, ptasks, blocks, lds, s);
+    if (st != LLMK_OK) return st;
+  }
+  return LLMK_OK;
+}

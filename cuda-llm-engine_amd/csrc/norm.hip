@@ -13,7 +13,7 @@
 // of the normal cache-allocation path measured 9% faster at [8192, 2048] than plain accesses. Rows wider than
 // 64 * 8 * 16 = 8192 values take a block-per-row kernel that reads the row twice (the second
 // time from L2).
-#include "common.hpp"
+#include "layer_ops.hpp"
 
 namespace llmk {
 
@@ -42,64 +42,22 @@ k_residual_add_scalar(const f16* a, const f16* b, f16* out, size_t n) {
 }
 
 // ----------------------------------------------------------------------------------------------
-// RMSNorm, one wave per row. VPL = 16-byte vectors per lane per tensor.
-// FUSED: resid <- fp16(resid + x) first, and the norm is taken of the updated resid.
-// FULL: vpr == 64 * VPL, every lane owns exactly VPL vectors (no bounds tests).
+// RMSNorm, one wave per row (the row body is layer_ops.hpp's rmsnorm_row). VPL = 16-byte
+// vectors per lane per tensor. FUSED: resid <- fp16(resid + x) first, and the norm is taken of
+// the updated resid. FULL: vpr == 64 * VPL, every lane owns exactly VPL vectors.
 // ----------------------------------------------------------------------------------------------
 template <int VPL, bool FUSED, bool FULL>
 __global__ void __launch_bounds__(256)
 k_rmsnorm_wave(const f16* x, f16* resid, const f16* __restrict__ w, f16* out, int n_rows,
                int vpr, float hidden_f, float eps, int wpb) {
-  const int lane = threadIdx.x & 63;
   // wpb (waves per block) is an argument, not blockDim: the arguments arrive preloaded in
   // SGPRs, blockDim would cost a scalar fetch before the first address is known.
   const int row = blockIdx.x * wpb + (threadIdx.x >> 6);
   if (row >= n_rows) return;  // uniform per wave
   const size_t base = (size_t)row * vpr * 8;
-  auto owned = [&](int v) { return FULL || v < vpr; };
-
-  f16x8 h[VPL], wv[VPL];
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + 64 * k;
-    if (owned(v)) {
-      h[k] = as_h8(ld16_stream(x + base + 8 * v));
-      if (FUSED) h[k] = as_h8(ld16_stream(resid + base + 8 * v)) + h[k];
-      wv[k] = as_h8(ld16(w + 8 * v));
-    } else {
-      h[k] = (f16x8)(f16)0;
-      wv[k] = (f16x8)(f16)0;
-    }
-  }
-  if (FUSED) {
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int v = lane + 64 * k;
-      if (owned(v)) st16_stream(resid + base + 8 * v, as_u4(h[k]));
-    }
-  }
-
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < VPL; ++k)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float f = (float)h[k][j];
-      ss = ss + f * f;
-    }
-  ss = wave_sum(ss);
-  const float inv = 1.0f / __builtin_sqrtf(ss / hidden_f + eps);
-
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int v = lane + 64 * k;
-    if (owned(v)) {
-      f16x8 a;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) a[j] = (f16)((float)h[k][j] * inv);
-      st16_stream(out + base + 8 * v, as_u4(wv[k] * a));
-    }
-  }
+  rmsnorm_row<VPL, FUSED, FULL>(x + base, FUSED ? resid + base : nullptr,
+                                FUSED ? resid + base : nullptr, w, out + base, vpr, hidden_f,
+                                eps, threadIdx.x & 63);
 }
 
 // Wide rows: one 256-thread block per row, two passes over the row.

@@ -253,6 +253,17 @@ typedef struct llmk_decode_pass {
 
 LLMK_API int llmk_decode_nongemm_pass(const llmk_decode_pass* pass, void* stream);
 
+/* The same pass and results with one launch per layer (n_layers launches instead of
+ * 1 + 3 * n_layers): a layer's add + RMSNorm rows, RoPE + K/V scatter tokens and SwiGLU chunks
+ * are blocks of one launch, and the embedding gather is fused into the first layer's residual
+ * add (the residual buffer never holds the bare embedding rows). Valid because the pass's
+ * per-layer inputs are independent of each other; in a decode step with GEMMs between these
+ * ops they are not, and the engine launches them one by one. Requires head_dim 64, hidden a
+ * power-of-two multiple of 512 up to 8192, (n_heads + 2 * n_kv_heads) * 8 <= 1024 and every
+ * pointer 16-byte aligned (LLMK_ERR_UNSUPPORTED / LLMK_ERR_ALIGNMENT otherwise: use
+ * llmk_decode_nongemm_pass). */
+LLMK_API int llmk_decode_nongemm_pass_layers(const llmk_decode_pass* pass, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * The decode step around the kernels above: projections (hipBLASLt), the fused layouts they
  * produce, and an engine that runs a whole Llama-3 forward pass over a batch of token rows.

@@ -181,6 +181,46 @@ def test_decode_pass_hip_graph_replays(llmk, orc, wl, inv):
             assert np.array_equal(a, b), f"replay {i}, output {j} differs from the eager pass"
 
 
+def _pass_pair(llmk, wl, inv, **kw):
+    """Two identical input sets of the decode pass (same seed) and their pass objects."""
+    out = []
+    for _ in range(2):
+        p = wl.decode_pass_inputs(inv[1], **kw)
+        dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables,
+                                    p.positions, p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
+                                    n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
+                                    page_size=wl.PAGE, max_pages=p.max_pages, eps=EPS)
+        out.append((p, dp))
+    return out
+
+
+@pytest.mark.parametrize("shape", [dict(n=64, layers=3, max_pages=32, seed=0x5EED0000 + 56),
+                                   dict(n=37, layers=2, max_pages=8, seed=0x5EED0000 + 57),
+                                   dict()])
+def test_decode_pass_one_launch_per_layer_gives_the_bits_of_the_op_by_op_pass(llmk, wl, inv,
+                                                                            shape):
+    """llmk_decode_nongemm_pass_layers (each layer's norm rows, RoPE + scatter tokens and SwiGLU
+    chunks in one launch, the embedding gather fused into the first residual add) against
+    llmk_decode_nongemm_pass on identical inputs: the residual, and every layer's normed rows,
+    rotated Q, SwiGLU output and whole K and V pools, bit for bit. Shapes: a small pass, a
+    ragged one (37 sequences: a partial last SwiGLU chunk), and config 5 (256 x 16 layers)."""
+    (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **shape)
+    for L in pa.per_layer:
+        L["act"].zero_()
+        L["normed"].zero_()
+    for L in pb.per_layer:
+        L["act"].fill_(float("nan"))
+        L["normed"].fill_(float("nan"))
+    pb.residual.fill_(float("nan"))
+    da.run()
+    db.run_layers()
+    torch.cuda.synchronize()
+    assert torch.equal(pa.residual.view(torch.int16), pb.residual.view(torch.int16))
+    for l, (A, B) in enumerate(zip(pa.per_layer, pb.per_layer)):
+        for key in ("normed", "q", "act", "k_pool", "v_pool"):
+            assert torch.equal(A[key].view(torch.int16), B[key].view(torch.int16)), (l, key)
+
+
 def test_cpp_dropin_binary():
     """Engine-style C++ through llmk.hpp (the reference's launcher names and argument lists)."""
     exe = os.path.join(ROOT, "tests", "cpp", "llmk_dropin_test")
