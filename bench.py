@@ -151,9 +151,15 @@ PROFILE_SHAPES = [
      3147904),
     ("decode:swiglu_256x8192", "pass_graph", "k_swiglu_vecILi1E", 4096 * 64, 12582912),
     # the pass with one launch per layer: 256 norm rows, 256 RoPE tokens, 4096 SwiGLU chunks
-    ("decode_layers:layer_256", "pass_layers", "k_layer_passILi4ELb0ELi6E", 4608 * 64,
-     4198400 + 3147904 + 12582912),
+    ("decode_layers:layer_256", "pass_layers", "k_layer_passILi4ELb0ELi6E|k_layer_pass<4, false, 6>",
+     4608 * 64, 4198400 + 3147904 + 12582912),
 ]
+
+
+def _name_matches(pattern: str, name: str) -> bool:
+    """`pattern`: substrings separated by '|', any of which may occur in the kernel name
+    (rocprofv3 prints some names mangled and some demangled)."""
+    return any(p in name for p in pattern.split("|"))
 
 
 def _grid(r) -> int:
@@ -205,7 +211,7 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
     avg = {k: sum(v) / len(v) for k, v in cnt.items() if v}
 
     def find(section, name, grid):
-        keys = [k for k in dur if k[0] == section and name in k[1] and k[2] == grid]
+        keys = [k for k in dur if k[0] == section and _name_matches(name, k[1]) and k[2] == grid]
         return keys[0] if keys else None
 
     print("# rocprofv3 summaries of bench.py on one MI355X (gfx950), made by:")
@@ -267,7 +273,7 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
     summarize_spread(tagged)
     print("#")
     summarize_pass(tagged, "pass_graph", "k_embedding", 49)
-    summarize_pass(tagged, "pass_layers", "k_layer_passILi4ELb1E", 16)
+    summarize_pass(tagged, "pass_layers", "k_layer_passILi4ELb1E|k_layer_pass<4, true", 16)
     return 1 if missing else 0
 
 
@@ -291,7 +297,7 @@ def summarize_spread(tagged):
     for label, sec, name, g, alg in PROFILE_SHAPES:
         if sec.startswith("pass") or "merge" in label:
             continue
-        keys = [k for k in by_sec if k[0] == sec and name in k[1] and k[2] == g]
+        keys = [k for k in by_sec if k[0] == sec and _name_matches(name, k[1]) and k[2] == g]
         if not keys:
             continue
         rows = by_sec[keys[0]]
@@ -318,7 +324,7 @@ def summarize_pass(tagged, section, first, launches):
     rows = [r for sec, r in tagged if sec == section and _own_kernel(r["Kernel_Name"])]
     passes, cur = [], None
     for r in rows:
-        if first in r["Kernel_Name"]:
+        if _name_matches(first, r["Kernel_Name"]):
             cur = []
             passes.append(cur)
         if cur is not None:
@@ -340,7 +346,9 @@ def summarize_pass(tagged, section, first, launches):
     n = len(passes)
     print(f"# {section}: {n} passes of {launches} kernels on the traced timeline: span "
           f"{span / n:.2f} us per pass = kernel durations {busy / n:.2f} us + gaps "
-          f"{(span - busy) / n:.2f} us")
+          f"{(span - busy) / n:.2f} us. Kernel tracing adds several us per dispatch of a graph "
+          f"(the gaps), so the span is no measure of the unprofiled pass; a kernel's duration "
+          f"includes its launch floor (an empty kernel's is 1.4-2.2 us).")
     for name, d in sorted(per_kernel.items(), key=lambda kv: -sum(kv[1])):
         print(f"#   {len(d) / n:6.2f} launches/pass x {sum(d) / len(d):7.3f} us = "
               f"{sum(d) / n:7.2f} us/pass  {name[:80]}")
@@ -759,8 +767,19 @@ class Bench:
         bd["stages"] = stages
         bd["sum_of_stages_us"] = round(sum(s["us"] for s in stages.values()), 3)
         bd["pass_minus_floor_us"] = round(bd["pass_us"] - bd["launch_floor_49_us"], 3)
-        log(f"    sum of stages {bd['sum_of_stages_us']:.2f} us; pass {bd['pass_us']:.2f} us = "
-            f"launch floor {bd['launch_floor_49_us']:.2f} + work {bd['pass_minus_floor_us']:.2f}")
+        # A graph launch costs more than a launch inside a graph: from the 1- and 49-kernel
+        # empty graphs, per launch = (floor_49 - floor_1) / 48, per graph = floor_1 - that. The
+        # four stage graphs pay three graph launches more than the one pass graph.
+        per_launch = (bd["launch_floor_49_us"] - stages["embedding"]["floor_us"]) / 48
+        per_graph = stages["embedding"]["floor_us"] - per_launch
+        bd["launch_us_in_graph"] = round(per_launch, 3)
+        bd["graph_launch_us"] = round(per_graph, 3)
+        bd["sum_of_stages_less_extra_graph_launches_us"] = round(
+            bd["sum_of_stages_us"] - 3 * per_graph, 3)
+        log(f"    sum of stages {bd['sum_of_stages_us']:.2f} us, less 3 extra graph launches of "
+            f"{per_graph:.2f} us: {bd['sum_of_stages_less_extra_graph_launches_us']:.2f} us; pass "
+            f"{bd['pass_us']:.2f} us = launch floor {bd['launch_floor_49_us']:.2f} "
+            f"({per_launch:.2f} us per launch) + work {bd['pass_minus_floor_us']:.2f}")
         entry["breakdown"] = bd
         del graphs, g_floor, dps, ps
         self.free()
