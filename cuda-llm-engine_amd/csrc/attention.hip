@@ -95,27 +95,68 @@ struct Chunk {
   u32x4 k[ROWS], v[ROWS];
 };
 
+// Where a block finds the pool page of the sequence's page i: its block-table row, read as each
+// chunk needs it ...
+struct TablePages {
+  const int* __restrict__ row;
+  __device__ __forceinline__ int operator()(int i) const { return row[i]; }
+};
+
+// ... or, for a run of at most kRunPages pages starting at page `first`, the run's entries read
+// once when the block starts, together with the sequence length. They are wave-uniform, so they
+// sit in scalar registers (four named members rather than an array, which the compiler would
+// place in memory to index it), and the pick is a chain of scalar selects. A chunk's loads then
+// wait for nothing but the length.
+constexpr int kRunPages = 4;
+struct RunPages {
+  int first, p0, p1, p2, p3;
+  // Entries of pages first .. first + 3, each index clamped to the row's width (the entries past
+  // the sequence's last page are read but never used).
+  __device__ __forceinline__ RunPages(const int* __restrict__ row, int first_page, int max_pages)
+      : first(first_page) {
+    const int last = max_pages - 1;
+    p0 = entry(row, first_page < last ? first_page : last);
+    p1 = entry(row, first_page + 1 < last ? first_page + 1 : last);
+    p2 = entry(row, first_page + 2 < last ? first_page + 2 : last);
+    p3 = entry(row, first_page + 3 < last ? first_page + 3 : last);
+  }
+  static __device__ __forceinline__ int entry(const int* __restrict__ row, int i) {
+    return row[i];
+  }
+  // Waits for the entries and `len` together. The compiler would otherwise sink each entry's
+  // load to its first use, behind the branch on the length, and the two round trips would
+  // follow one another.
+  __device__ __forceinline__ void settle(int& len) {
+    asm volatile("" : "+s"(p0), "+s"(p1), "+s"(p2), "+s"(p3), "+s"(len));
+  }
+  __device__ __forceinline__ int operator()(int i) const {
+    const int k = i - first;
+    const int a = __builtin_amdgcn_readfirstlane(p0), b = __builtin_amdgcn_readfirstlane(p1);
+    const int c = __builtin_amdgcn_readfirstlane(p2), d = __builtin_amdgcn_readfirstlane(p3);
+    return k == 0 ? a : k == 1 ? b : k == 2 ? c : d;
+  }
+};
+
 // Element offset of the first row of the chunk that starts at row `row0` of the block's position
-// range [pos0, ...): its page from the block table (wave-uniform, so the pool address of the
-// chunk stays in scalar registers and each lane adds only its 32-bit offset).
-template <int KVW>
-__device__ __forceinline__ size_t chunk_base(const int* __restrict__ table, int pos0, int row0,
+// range [pos0, ...): its page from `pages` (wave-uniform, so the pool address of the chunk stays
+// in scalar registers and each lane adds only its 32-bit offset).
+template <int KVW, class Pages>
+__device__ __forceinline__ size_t chunk_base(const Pages& pages, int pos0, int row0,
                                              size_t row_halves) {
   const int cpos = pos0 + row0 * (8 / KVW);  // first position of the chunk
-  const int page = table[cpos / kPage];
+  const int page = pages(cpos / kPage);
   return ((size_t)page * kPage + (size_t)(cpos % kPage)) * row_halves;
 }
 
 // Issues the loads of a chunk whose every position is cached (unconditional, so that the loads
 // of the next chunk can be in flight while this one is folded). lane_off: the lane's element
 // offset inside the first row; row_step: elements from one row read to the next.
-template <int KVW>
+template <int KVW, class Pages>
 __device__ __forceinline__ void load_chunk(Chunk<KVW>& c, const f16* __restrict__ k_pool,
-                                           const f16* __restrict__ v_pool,
-                                           const int* __restrict__ table, int pos0, int row0,
-                                           size_t row_halves, uint32_t lane_off,
-                                           uint32_t row_step) {
-  const size_t base = chunk_base<KVW>(table, pos0, row0, row_halves);
+                                           const f16* __restrict__ v_pool, const Pages& pages,
+                                           int pos0, int row0, size_t row_halves,
+                                           uint32_t lane_off, uint32_t row_step) {
+  const size_t base = chunk_base<KVW>(pages, pos0, row0, row_halves);
   const f16* kb = k_pool + base;
   const f16* vb = v_pool + base;
 #pragma unroll
@@ -184,19 +225,19 @@ __device__ __forceinline__ void fold_chunk(SoftmaxState& st, const u32x4 (&qv)[k
 
 // The one chunk of a wave that holds uncached positions: rows [row0, row0 + ROWS) of the block's
 // range [pos0, pos1), only the cached positions loaded.
-template <int KVW>
+template <int KVW, class Pages>
 __device__ __forceinline__ void attend_partial_chunk(SoftmaxState& st,
                                                      const u32x4 (&qv)[kGroup],
                                                      const f16* __restrict__ k_pool,
                                                      const f16* __restrict__ v_pool,
-                                                     const int* __restrict__ table, int pos0,
-                                                     int pos1, int row0, size_t row_halves,
+                                                     const Pages& pages, int pos0, int pos1,
+                                                     int row0, size_t row_halves,
                                                      uint32_t lane_off, uint32_t row_step,
                                                      int slot) {
   constexpr int PPL = 8 / KVW;
   constexpr int ROWS = Chunk<KVW>::ROWS;
   const int cpos = pos0 + row0 * PPL;
-  const size_t base = chunk_base<KVW>(table, pos0, row0, row_halves);
+  const size_t base = chunk_base<KVW>(pages, pos0, row0, row_halves);
   Chunk<KVW> c;
   bool ok[ROWS];
 #pragma unroll
@@ -223,22 +264,34 @@ struct MergeLds {
   float m[NP][HEADS], l[NP][HEADS];
 };
 
-// The block's attention over positions [pos0, pos1) of sequence `seq` (all cached, in the pages
-// of `table`) for the query heads of kv group `kvg`. On return thread t with t / 8 < HEADS holds
-// the block's combined unnormalised state of query head kvg * HEADS + t / 8, dims 8 * (t % 8)
-// .. + 8: A (sum of p * v), M (max score, log2 units) and L (sum of p). Ends with a barrier, so
-// the LDS can be reused at once.
+// The lane's 8 dims of the 4 query heads that share its kv head (kv head kvg * 8 + octet % KVW)
+// for sequence `seq`.
+template <int KVW>
+__device__ __forceinline__ void load_query(u32x4 (&qv)[kGroup], const f16* __restrict__ q,
+                                           int seq, int kvg, int n_heads) {
+  const int lane = threadIdx.x & 63;
+  const int kvh = kvg * 8 + (lane >> 3) % KVW;
+#pragma unroll
+  for (int i = 0; i < kGroup; ++i)
+    qv[i] = ld16(q + ((size_t)seq * n_heads + kvh * kGroup + i) * kHeadDim + (lane & 7) * 8);
+}
+
+// The block's attention over positions [pos0, pos1) of one sequence (all cached, in the pool
+// pages that `pages` names) for the query heads of kv group `kvg`, with the lane's query dims in
+// qv (load_query). On return thread t with t / 8 < HEADS holds the block's combined
+// unnormalised state of query head kvg * HEADS + t / 8, dims 8 * (t % 8) .. + 8: A (sum of
+// p * v), M (max score, log2 units) and L (sum of p). Ends with a barrier, so the LDS can be
+// reused at once.
 // NJ > 0: the wave has at most NJ chunks whose every position is cached; their loads are all
 // issued before the first fold (one round trip for a short segment). NJ = 0: any number, streamed
 // two at a time.
-template <int KVW, int NJ = 0>
-__device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
+template <int KVW, int NJ = 0, class Pages>
+__device__ __forceinline__ void attend_segment(const u32x4 (&qv)[kGroup],
                                                const f16* __restrict__ k_pool,
                                                const f16* __restrict__ v_pool,
-                                               const int* __restrict__ table, int seq, int pos0,
-                                               int pos1, int kvg, int n_heads, int n_kv_heads,
-                                               MergeLds<KVW>& lds, float (&A)[8], float& M,
-                                               float& L) {
+                                               const Pages& pages, int pos0, int pos1, int kvg,
+                                               int n_kv_heads, MergeLds<KVW>& lds,
+                                               float (&A)[8], float& M, float& L) {
   constexpr int PPL = 8 / KVW;
   constexpr int NP = MergeLds<KVW>::NP, HEADS = MergeLds<KVW>::HEADS;
   constexpr int ROWS = chunk_rows<KVW>();
@@ -246,17 +299,11 @@ __device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int octet = lane >> 3, d8 = lane & 7;
   const int slot = octet / KVW, kvl = octet % KVW;
-  const int kvh = kvg * 8 + kvl;
   const size_t row_halves = (size_t)n_kv_heads * kHeadDim;
   // Lane's offset inside a row read: this kv group's 8 heads, then 16 bytes per lane (for
   // KVW < 8 the lanes run on into the next PPL - 1 rows, which are contiguous within a page).
   const uint32_t lane_off = (uint32_t)(kvg * 8 * kHeadDim + lane * 8);
   const uint32_t row_step = (uint32_t)(PPL * row_halves);
-
-  u32x4 qv[kGroup];
-#pragma unroll
-  for (int i = 0; i < kGroup; ++i)
-    qv[i] = ld16(q + ((size_t)seq * n_heads + kvh * kGroup + i) * kHeadDim + d8 * 8);
 
   SoftmaxState st;
 #pragma unroll
@@ -286,7 +333,7 @@ __device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
       Chunk<KVW> c[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
-        load_chunk<KVW>(c[j], k_pool, v_pool, table, pos0, first + (j < nj ? j : nj - 1) * STEP,
+        load_chunk<KVW>(c[j], k_pool, v_pool, pages, pos0, first + (j < nj ? j : nj - 1) * STEP,
                         row_halves, lane_off, row_step);
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
@@ -294,19 +341,19 @@ __device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
     }
   } else if (nj > 0) {
     Chunk<KVW> a, b;
-    load_chunk<KVW>(a, k_pool, v_pool, table, pos0, first, row_halves, lane_off,
+    load_chunk<KVW>(a, k_pool, v_pool, pages, pos0, first, row_halves, lane_off,
                     row_step);
     int j = 1, r = first + STEP;
     for (; j + 1 < nj; j += 2, r += 2 * STEP) {
-      load_chunk<KVW>(b, k_pool, v_pool, table, pos0, r, row_halves, lane_off,
+      load_chunk<KVW>(b, k_pool, v_pool, pages, pos0, r, row_halves, lane_off,
                       row_step);
       fold_chunk<KVW, true>(st, qv, a, all);
-      load_chunk<KVW>(a, k_pool, v_pool, table, pos0, r + STEP, row_halves,
+      load_chunk<KVW>(a, k_pool, v_pool, pages, pos0, r + STEP, row_halves,
                       lane_off, row_step);
       fold_chunk<KVW, true>(st, qv, b, all);
     }
     if (j < nj) {
-      load_chunk<KVW>(b, k_pool, v_pool, table, pos0, r, row_halves, lane_off,
+      load_chunk<KVW>(b, k_pool, v_pool, pages, pos0, r, row_halves, lane_off,
                       row_step);
       fold_chunk<KVW, true>(st, qv, a, all);
       fold_chunk<KVW, true>(st, qv, b, all);
@@ -316,7 +363,7 @@ __device__ __forceinline__ void attend_segment(const f16* __restrict__ q,
   }
   const int row0 = first + nj * STEP;
   if (row0 < n_rows)  // at most one partly cached chunk per wave
-    attend_partial_chunk<KVW>(st, qv, k_pool, v_pool, table, pos0, pos1, row0, row_halves,
+    attend_partial_chunk<KVW>(st, qv, k_pool, v_pool, pages, pos0, pos1, row0, row_halves,
                               lane_off, row_step, slot);
 
   // Merge the NP partial states of every query head through LDS.
@@ -378,31 +425,52 @@ __device__ __forceinline__ void store_nan(f16* __restrict__ out, int seq, int h,
 
 // Sequence-split grid (num_splits, kv groups, n_seq): block (split, g, s) takes pages
 // [split * pages_per_split, +pages_per_split) of sequence s. Used with one or two splits, and for
-// small batches cut into runs of at most 4 pages (NJ: as in attend_segment).
-template <int KVW, int NJ>
+// small batches cut into runs of at most kRunPages pages (NJ: as in attend_segment). RUN: the
+// runs are that short, and the block reads its query, the sequence length and its run's
+// block-table entries all at once, so that its first K/V loads follow one round trip.
+// The arguments are ordered so that those the block needs before its first K/V loads fill the
+// 16 kernel-argument dwords preloaded into scalar registers; the output pointers, needed last,
+// are read from the argument buffer.
+template <int KVW, int NJ, bool RUN>
 __global__ void __launch_bounds__(kThreads)
-k_attn_split(const f16* __restrict__ q, const f16* __restrict__ k_pool,
-             const f16* __restrict__ v_pool, const int* __restrict__ block_tables,
-             const int* __restrict__ seq_lens, f16* __restrict__ out, float* __restrict__ part_o,
-             float2* __restrict__ part_ml, int max_pages, int n_heads, int n_kv_heads,
-             int num_splits, int pages_per_split) {
+k_attn_split(const int* __restrict__ block_tables, const int* __restrict__ seq_lens,
+             int max_pages, int pages_per_split, int n_heads, int n_kv_heads, int num_splits,
+             const f16* __restrict__ q, const f16* __restrict__ k_pool,
+             const f16* __restrict__ v_pool, f16* __restrict__ out, float* __restrict__ part_o,
+             float2* __restrict__ part_ml) {
   __shared__ MergeLds<KVW> lds;
   const int split = blockIdx.x, kvg = blockIdx.y, seq = blockIdx.z;
-  const int S = seq_lens[seq];
-  const int P = seq_pages(S, max_pages);
+  const int* __restrict__ row = block_tables + (size_t)seq * max_pages;
   const int page0 = split * pages_per_split;
+  // RUN: the run's page entries, read ahead of the length (unused, and dropped, otherwise).
+  RunPages run(row, RUN ? page0 : 0, RUN ? max_pages : 1);
+  int S = seq_lens[seq];
+  if constexpr (RUN) run.settle(S);
+  const int P = seq_pages(S, max_pages);
   const int h = kvg * MergeLds<KVW>::HEADS + (threadIdx.x >> 3);
   const bool writer = (int)(threadIdx.x >> 3) < MergeLds<KVW>::HEADS && h < n_heads;
-  if (page0 >= P) {
-    // No cached position: the quotient 0 / 0 of an all-empty merge, as the reference yields.
-    if (split == 0 && writer) store_nan(out, seq, h, n_heads);
-    return;
-  }
   const int page1 = page0 + pages_per_split < P ? page0 + pages_per_split : P;
   const int pos1 = S < page1 * kPage ? S : page1 * kPage;
   float A[8], M, L;
-  attend_segment<KVW, NJ>(q, k_pool, v_pool, block_tables + (size_t)seq * max_pages, seq,
-                          page0 * kPage, pos1, kvg, n_heads, n_kv_heads, lds, A, M, L);
+  u32x4 qv[kGroup];
+  if constexpr (RUN) {
+    load_query<KVW>(qv, q, seq, kvg, n_heads);
+    if (page0 >= P) {
+      // No cached position: the quotient 0 / 0 of an all-empty merge, as the reference yields.
+      if (split == 0 && writer) store_nan(out, seq, h, n_heads);
+      return;
+    }
+    attend_segment<KVW, NJ>(qv, k_pool, v_pool, run, page0 * kPage, pos1, kvg, n_kv_heads, lds,
+                            A, M, L);
+  } else {
+    if (page0 >= P) {
+      if (split == 0 && writer) store_nan(out, seq, h, n_heads);
+      return;
+    }
+    load_query<KVW>(qv, q, seq, kvg, n_heads);
+    attend_segment<KVW, NJ>(qv, k_pool, v_pool, TablePages{row}, page0 * kPage, pos1, kvg,
+                            n_kv_heads, lds, A, M, L);
+  }
   if (!writer) return;
   if ((P + pages_per_split - 1) / pages_per_split == 1)
     store_out(out, seq, h, n_heads, A, L);
@@ -541,8 +609,10 @@ k_attn_balanced(const f16* __restrict__ q, const f16* __restrict__ k_pool,
       const int lp0 = (g0 > gs ? g0 : gs) - gs, lp1 = (g1 < gs + P ? g1 : gs + P) - gs;
       const int pos1 = S < lp1 * kPage ? S : lp1 * kPage;
       float A[8], M, L;
-      attend_segment<KVW>(q, k_pool, v_pool, block_tables + (size_t)s * max_pages, s,
-                          lp0 * kPage, pos1, kvg, n_heads, n_kv_heads, lds, A, M, L);
+      u32x4 qv[kGroup];
+      load_query<KVW>(qv, q, s, kvg, n_heads);
+      attend_segment<KVW>(qv, k_pool, v_pool, TablePages{block_tables + (size_t)s * max_pages},
+                          lp0 * kPage, pos1, kvg, n_kv_heads, lds, A, M, L);
       const int first = gs / qp, n_seg = (gs + P - 1) / qp - first + 1, k = b - first;
       if (writer) {
         if (n_seg == 1)
@@ -805,7 +875,7 @@ struct AttnArgs {
 // grid, which follows the actual lengths. Measured at 8 sequences of lengths uniform in
 // [1, 2048], both kernels together: 12.1 us with 4-page runs against 16.1 us page-balanced.
 constexpr int kSplitGridPairs = 16;
-constexpr int kShortRunPages = 4;
+constexpr int kShortRunPages = kRunPages;
 
 // attend_segment's NJ for runs of pps pages: all of a wave's chunks in flight at once when it
 // has at most two (4 chunks cost 188 VGPRs, and the lost occupancy outweighed the gain), else 0.
@@ -817,12 +887,12 @@ int short_run_chunks(int pps) {
   return per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : 0;
 }
 
-template <int KVW, int NJ>
+template <int KVW, int NJ, bool RUN>
 int split_launch(const AttnArgs& a, int groups, int pps, hipStream_t s) {
   const dim3 grid((unsigned)a.num_splits, (unsigned)groups, (unsigned)a.n_seq);
-  return launch(k_attn_split<KVW, NJ>, grid, dim3(kThreads), 0, s, a.q, a.k_pool, a.v_pool,
-                a.tables, a.lens, a.out, a.part_o, a.part_ml, a.max_pages, a.n_heads,
-                a.n_kv_heads, a.num_splits, pps);
+  return launch(k_attn_split<KVW, NJ, RUN>, grid, dim3(kThreads), 0, s, a.tables, a.lens,
+                a.max_pages, pps, a.n_heads, a.n_kv_heads, a.num_splits, a.q, a.k_pool, a.v_pool,
+                a.out, a.part_o, a.part_ml);
 }
 
 template <int KVW>
@@ -845,12 +915,12 @@ int attn_launch(const AttnArgs& a, hipStream_t s) {
   int st;
   if (short_runs) {
     switch (short_run_chunks<KVW>(pps)) {
-      case 1: st = split_launch<KVW, 1>(a, groups, pps, s); break;
-      case 2: st = split_launch<KVW, 2>(a, groups, pps, s); break;
-      default: st = split_launch<KVW, 0>(a, groups, pps, s); break;
+      case 1: st = split_launch<KVW, 1, true>(a, groups, pps, s); break;
+      case 2: st = split_launch<KVW, 2, true>(a, groups, pps, s); break;
+      default: st = split_launch<KVW, 0, true>(a, groups, pps, s); break;
     }
   } else {
-    st = split_launch<KVW, 0>(a, groups, pps, s);
+    st = split_launch<KVW, 0, false>(a, groups, pps, s);
   }
   if (st != 0 || pps >= a.max_pages) return st;  // every sequence fits in one split
   if (short_runs) {
