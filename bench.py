@@ -124,6 +124,9 @@ def read_traffic() -> dict:
 ATTN_BYTES_256 = 546_019_628
 ATTN_BYTES_16x2048 = 67_248_192  # 16 sequences x 2048 positions
 
+# Kernel rows listed per section in the profile summary.
+SECTION_ROWS = 12
+
 # (label, section, kernel-name substring, grid size in work-items, algorithmic bytes) of each
 # measured launch shape whose counters are reported; grid sizes follow from the launchers'
 # grid choices at the benchmark shapes.
@@ -254,7 +257,10 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
         print(line)
     print("#")
     print("# The libllmk and hipBLASLt kernels of every section (input generation and the timer's")
-    print("# spin kernel left out): calls, mean / min / max duration (us), grid (work-items), kernel.")
+    print("# spin kernel left out): calls, mean / min / max duration (us), grid (work-items), kernel;")
+    print(f"# the {SECTION_ROWS} (kernel, grid) pairs with the most time per section, the rest in one")
+    print("# line (in the argmax section: the engine's start-up, whose GEMM plan search times every")
+    print("# candidate hipBLASLt solution a few times).")
     sections = []
     for k in dur:
         if k[0] not in sections:
@@ -264,10 +270,15 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
         if not ks:
             continue
         print(f"## section {sec}")
-        for k in sorted(ks, key=lambda k: -sum(dur[k])):
+        ks.sort(key=lambda k: -sum(dur[k]))
+        for k in ks[:SECTION_ROWS]:
             d = dur[k]
             print(f"#   {len(d):6d} {sum(d) / len(d):9.3f} {min(d):9.3f} {max(d):9.3f} "
                   f"{k[2]:9d}  {k[1][:96]}")
+        rest = ks[SECTION_ROWS:]
+        if rest:
+            print(f"#   ... {len(rest)} more pairs: {sum(len(dur[k]) for k in rest)} launches, "
+                  f"{sum(sum(dur[k]) for k in rest):.1f} us in all")
     print("#")
     tagged = _by_section(_csv_rows(trace_dir, "kernel_trace.csv"))
     summarize_spread(tagged)
