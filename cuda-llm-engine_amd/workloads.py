@@ -230,7 +230,10 @@ class DecodePassInputs:
 
 
 def decode_pass_inputs(inv_freq: torch.Tensor, n=256, layers=LAYERS, max_pages=128,
-                       table=None, seed=SEED_BASE + 5, device="cuda") -> DecodePassInputs:
+                       table=None, seed=SEED_BASE + 5, device="cuda", hidden=HIDDEN,
+                       n_heads=N_HEADS, n_kv=N_KV, inter=INTER,
+                       vocab=VOCAB) -> DecodePassInputs:
+    """Config 5's inputs (by default); the model dimensions can be changed for shape tests."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(1, max_pages * PAGE + 1, n)
     npages = (lens + PAGE - 1) // PAGE
@@ -243,27 +246,27 @@ def decode_pass_inputs(inv_freq: torch.Tensor, n=256, layers=LAYERS, max_pages=1
         off += p
     g = _gen(seed, device)
     if table is None:
-        table = embedding_table(device=device)
+        table = embedding_table(vocab, hidden, device=device)
     ids = torch.randint(0, table.shape[0], (n,), generator=g, device=device, dtype=torch.int32)
-    kvdim = N_KV * HEAD_DIM
+    kvdim = n_kv * HEAD_DIM
     per_layer = []
     for _ in range(layers):
         per_layer.append(dict(
-            x=normal_f16((n, HIDDEN), g, device),
-            norm_w=normal_f16((HIDDEN,), g, device, 1.0, 0.1),
-            normed=torch.empty((n, HIDDEN), dtype=torch.float16, device=device),
-            q=normal_f16((n, N_HEADS, HEAD_DIM), g, device),
-            k=normal_f16((n, N_KV, HEAD_DIM), g, device),
-            v=normal_f16((n, N_KV, HEAD_DIM), g, device),
+            x=normal_f16((n, hidden), g, device),
+            norm_w=normal_f16((hidden,), g, device, 1.0, 0.1),
+            normed=torch.empty((n, hidden), dtype=torch.float16, device=device),
+            q=normal_f16((n, n_heads, HEAD_DIM), g, device),
+            k=normal_f16((n, n_kv, HEAD_DIM), g, device),
+            v=normal_f16((n, n_kv, HEAD_DIM), g, device),
             k_pool=poisoned(total * PAGE * kvdim, device),
             v_pool=poisoned(total * PAGE * kvdim, device),
-            gate=normal_f16((n, INTER), g, device),
-            up=normal_f16((n, INTER), g, device),
-            act=torch.empty((n, INTER), dtype=torch.float16, device=device)))
+            gate=normal_f16((n, inter), g, device),
+            up=normal_f16((n, inter), g, device),
+            act=torch.empty((n, inter), dtype=torch.float16, device=device)))
     return DecodePassInputs(
         n=n, layers=layers, max_pages=max_pages, total_pages=total, lens=lens,
         tables_host=tables, table=table, token_ids=ids,
-        residual=torch.empty((n, HIDDEN), dtype=torch.float16, device=device),
+        residual=torch.empty((n, hidden), dtype=torch.float16, device=device),
         block_tables=torch.from_numpy(tables).to(device),
         positions=torch.from_numpy((lens - 1).astype(np.int32)).to(device),
         inv_freq=inv_freq, per_layer=per_layer)

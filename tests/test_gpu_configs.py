@@ -187,24 +187,18 @@ def _pass_pair(llmk, wl, inv, **kw):
     for _ in range(2):
         p = wl.decode_pass_inputs(inv[1], **kw)
         dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables,
-                                    p.positions, p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
-                                    n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
-                                    page_size=wl.PAGE, max_pages=p.max_pages, eps=EPS)
+                                    p.positions, p.inv_freq, p.per_layer,
+                                    n_heads=kw.get("n_heads", wl.N_HEADS),
+                                    n_kv_heads=kw.get("n_kv", wl.N_KV), head_dim=wl.HEAD_DIM,
+                                    inter=kw.get("inter", wl.INTER), page_size=wl.PAGE,
+                                    max_pages=p.max_pages, eps=EPS)
         out.append((p, dp))
     return out
 
 
-@pytest.mark.parametrize("shape", [dict(n=64, layers=3, max_pages=32, seed=0x5EED0000 + 56),
-                                   dict(n=37, layers=2, max_pages=8, seed=0x5EED0000 + 57),
-                                   dict()])
-def test_decode_pass_one_launch_per_layer_gives_the_bits_of_the_op_by_op_pass(llmk, wl, inv,
-                                                                            shape):
-    """llmk_decode_nongemm_pass_layers (each layer's norm rows, RoPE + scatter tokens and SwiGLU
-    chunks in one launch, the embedding gather fused into the first residual add) against
-    llmk_decode_nongemm_pass on identical inputs: the residual, and every layer's normed rows,
-    rotated Q, SwiGLU output and whole K and V pools, bit for bit. Shapes: a small pass, a
-    ragged one (37 sequences: a partial last SwiGLU chunk), and config 5 (256 x 16 layers)."""
-    (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **shape)
+def _same_pass_bits(pa, da, pb, db):
+    """Runs the op-by-op pass on set a and the one-launch-per-layer pass on set b (whose
+    outputs start as NaN) and compares every output bit for bit."""
     for L in pa.per_layer:
         L["act"].zero_()
         L["normed"].zero_()
@@ -219,6 +213,57 @@ def test_decode_pass_one_launch_per_layer_gives_the_bits_of_the_op_by_op_pass(ll
     for l, (A, B) in enumerate(zip(pa.per_layer, pb.per_layer)):
         for key in ("normed", "q", "act", "k_pool", "v_pool"):
             assert torch.equal(A[key].view(torch.int16), B[key].view(torch.int16)), (l, key)
+
+
+@pytest.mark.parametrize("shape", [dict(n=64, layers=3, max_pages=32, seed=0x5EED0000 + 56),
+                                   dict(n=37, layers=2, max_pages=8, seed=0x5EED0000 + 57),
+                                   dict()])
+def test_decode_pass_one_launch_per_layer_gives_the_bits_of_the_op_by_op_pass(llmk, wl, inv,
+                                                                            shape):
+    """llmk_decode_nongemm_pass_layers (each layer's norm rows, RoPE + scatter tokens and SwiGLU
+    chunks in one launch, the embedding gather fused into the first residual add) against
+    llmk_decode_nongemm_pass on identical inputs: the residual, and every layer's normed rows,
+    rotated Q, SwiGLU output and whole K and V pools, bit for bit. Shapes: a small pass, a
+    ragged one (37 sequences: a partial last SwiGLU chunk), and config 5 (256 x 16 layers)."""
+    (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **shape)
+    _same_pass_bits(pa, da, pb, db)
+
+
+# (hidden, n_heads, n_kv, inter): every row width the launch takes (hidden / 512 = 1, 2, 4, 8,
+# 16 vectors per lane) and every RoPE task count it compiles (16-byte vectors per token over 64
+# lanes: 2, 3, 8, 10, 16 and 12 tasks, run as 6, 6, 8, 12, 16 and 12).
+PASS_MODELS = [(512, 8, 2, 1376), (1024, 16, 4, 2816), (2048, 48, 8, 5632),
+               (4096, 64, 8, 11008), (8192, 112, 8, 8192), (2048, 64, 16, 4096)]
+
+
+@pytest.mark.parametrize("model", PASS_MODELS, ids=lambda m: "h%d_q%d_kv%d" % m[:3])
+def test_decode_pass_one_launch_per_layer_across_model_shapes(llmk, wl, inv, model):
+    """The one-launch-per-layer pass against the op-by-op pass (each of whose kernels is checked
+    against the oracle on its own) at other model dimensions than config 5's: 29 sequences
+    (a partial last SwiGLU chunk), 2 layers, bit for bit."""
+    hidden, nh, nkv, inter = model
+    kw = dict(n=29, layers=2, max_pages=8, seed=0x5EED0000 + 58, hidden=hidden, n_heads=nh,
+              n_kv=nkv, inter=inter, vocab=1000)
+    (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **kw)
+    _same_pass_bits(pa, da, pb, db)
+
+
+def test_decode_pass_one_launch_per_layer_refuses_other_shapes(llmk, wl, inv):
+    """Shapes outside the single launch's (a head_dim other than 64, a hidden size that is not
+    512 times a power of two up to 8192) are refused with LLMK_ERR_UNSUPPORTED, and the
+    op-by-op pass still takes them."""
+    p = wl.decode_pass_inputs(inv[1], n=5, layers=1, max_pages=4, seed=0x5EED0000 + 59,
+                              hidden=1536, vocab=100)
+    dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables, p.positions,
+                                p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
+                                n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
+                                page_size=wl.PAGE, max_pages=p.max_pages, eps=EPS)
+    with pytest.raises(llmk.LlmkError) as err:
+        dp.run_layers()
+    assert err.value.status == llmk.LLMK_ERR_UNSUPPORTED
+    dp.run()
+    torch.cuda.synchronize()
+    assert torch.isfinite(p.residual).all()
 
 
 def test_cpp_dropin_binary():
