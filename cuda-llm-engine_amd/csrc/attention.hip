@@ -538,13 +538,14 @@ constexpr int kPrologueTiles = 4;
 // holding a sequence's first segment records there how many segments it has. A sequence with a
 // single segment gets its output written here; the merge kernel finishes the others and writes
 // the NaN of empty sequences.
+// Argument order as in k_attn_split: what the prologue needs first sits in the preloaded dwords.
 template <int KVW>
 __global__ void __launch_bounds__(kThreads)
-k_attn_balanced(const f16* __restrict__ q, const f16* __restrict__ k_pool,
-                const f16* __restrict__ v_pool, const int* __restrict__ block_tables,
-                const int* __restrict__ seq_lens, f16* __restrict__ out,
-                float* __restrict__ part_o, float2* __restrict__ part_ml, int n_seq,
-                int max_pages, int n_heads, int n_kv_heads, int num_splits, int n_blocks) {
+k_attn_balanced(const int* __restrict__ seq_lens, const int* __restrict__ block_tables,
+                int n_seq, int max_pages, int n_heads, int n_kv_heads, int num_splits,
+                int n_blocks, const f16* __restrict__ q, const f16* __restrict__ k_pool,
+                const f16* __restrict__ v_pool, f16* __restrict__ out,
+                float* __restrict__ part_o, float2* __restrict__ part_ml) {
   __shared__ MergeLds<KVW> lds;
   __shared__ int red[2 * kWaves];
   __shared__ int found[2];
@@ -905,8 +906,8 @@ int attn_launch(const AttnArgs& a, hipStream_t s) {
     int blocks = resident_blocks<KVW>() / groups;
     if (blocks < 1) blocks = 1;
     int st = launch(k_attn_balanced<KVW>, dim3((unsigned)blocks, (unsigned)groups), dim3(kThreads),
-                    0, s, a.q, a.k_pool, a.v_pool, a.tables, a.lens, a.out, a.part_o, a.part_ml,
-                    a.n_seq, a.max_pages, a.n_heads, a.n_kv_heads, a.num_splits, blocks);
+                    0, s, a.lens, a.tables, a.n_seq, a.max_pages, a.n_heads, a.n_kv_heads,
+                    a.num_splits, blocks, a.q, a.k_pool, a.v_pool, a.out, a.part_o, a.part_ml);
     if (st != 0) return st;
     const dim3 mgrid((unsigned)((a.n_heads + 31) / 32), (unsigned)a.n_seq);
     return launch(k_attn_merge, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, a.lens, a.out,
