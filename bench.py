@@ -57,7 +57,7 @@ SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_819
             "pass_stage_add_rmsnorm", "pass_stage_rope_kv_scatter", "pass_stage_swiglu",
             "pass_floor_stages", "attention_256", "attention_16x2048", "attention_sweep",
             "argmax", "step_256", "step_8", "sched", "probe_sweep", "probe_kernels", "copy_1GiB",
-            "end"]
+            "residual_add", "rmsnorm_8192", "kv_scatter_8192", "kv_scatter_batch_256", "end"]
 
 # Launch shapes (blocks, threads) of the 16-layer pass at 256 sequences, from the launchers'
 # grid rules: the embedding and add+RMSNorm take one 64-thread wave per row below 4096 rows
@@ -80,13 +80,14 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--kernels", default="all",
                     choices=["all", "kernels", "headline", "configs", "pass", "attn", "probe",
-                             "step", "step8", "sched"],
+                             "step", "step8", "sched", "rows"],
                     help="all: everything; kernels: all but the engine step and the scheduler "
                          "(for counter runs); headline: config 2 only; configs: configs 1-4, the "
                          "pass and the probes; pass: the decode pass and its breakdown; attn: decode "
                          "attention and its batch sweep; probe: bandwidth probes; step / step8: "
                          "the engine's decode step of 256 / 8 sequences; sched: the reference's "
-                         "scheduler workload (config 2 is always measured)")
+                         "scheduler workload; rows: residual_add, RMSNorm [8192,2048] and the "
+                         "two scatters (config 2 is always measured)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-seconds", type=float, default=3.0,
                     help="CPU time per configuration (all cores 70%%, one core 30%%)")
@@ -661,6 +662,88 @@ class Bench:
         self.free()
         return table
 
+    # ------------------------------------------------------------------ rows a2, a3, a8, a9
+    def other_rows(self):
+        """The scope rows no configuration times on its own: residual_add (in place, as the
+        reference's engine calls it) and RMSNorm at config 2's shape, the prefill scatter of
+        8192 rows into a shuffled 512-page table, and the decode scatter of 256 sequences
+        (lengths uniform in [1, 2048], pages shuffled over the batch's pool)."""
+        wl, llmk, np, torch = self.wl, self.llmk, self.np, self.torch
+        rows, H = 8192, wl.HIDDEN
+        n = rows * H
+        R = sets_for(3 * n * 2)
+        sets = [wl.add_rmsnorm_inputs(rows, H, seed=wl.SEED_BASE + 60 + 100 * i)
+                for i in range(R)]
+        self.cpu_inputs["residual_add_8192x2048"] = {
+            k: sets[0][k].cpu().numpy().view(np.uint16).copy() for k in ("residual", "x", "w")}
+        self.cpu_inputs["rmsnorm_8192x2048"] = self.cpu_inputs["residual_add_8192x2048"]
+        self.mark("residual_add")
+        t = self.run(lambda i: llmk.residual_add(sets[i]["residual"], sets[i]["x"],
+                                                 sets[i]["residual"], n), R)
+        self.kernels["residual_add_8192x2048"] = kernel_entry(
+            "residual_add [8192,2048] in place", wl.bytes_residual_add(n), t,
+            self.traffic.get("residual_add_8192x2048"), {"sets": R})
+        self.mark("rmsnorm_8192")
+        t = self.run(lambda i: llmk.rmsnorm(sets[i]["x"], sets[i]["w"], sets[i]["out"], rows, H,
+                                            wl.EPS), R)
+        self.kernels["rmsnorm_8192x2048"] = kernel_entry(
+            "rmsnorm [8192,2048]", wl.bytes_rmsnorm(rows, H), t,
+            self.traffic.get("rmsnorm_8192x2048"), {"sets": R})
+        del sets
+        self.free()
+
+        kvdim, ps = wl.N_KV * wl.HEAD_DIM, wl.PAGE
+        T, pages = 8192, 8192 // wl.PAGE
+        nb = wl.bytes_kv_scatter(T, kvdim, ps)
+        R = sets_for(nb)
+        rng = np.random.default_rng(wl.SEED_BASE + 70)
+        g = torch.Generator(device=self.dev).manual_seed(wl.SEED_BASE + 71)
+        sc = []
+        for _ in range(R):
+            sc.append(dict(src=wl.normal_f16((T, kvdim), g, self.dev),
+                           pool=wl.poisoned(pages * ps * kvdim, self.dev),
+                           table=torch.from_numpy(rng.permutation(pages).astype(np.int32))
+                           .to(self.dev)))
+        self.cpu_inputs["kv_scatter_8192"] = {
+            "src": sc[0]["src"].cpu().numpy().view(np.uint16).copy(),
+            "table": sc[0]["table"].cpu().numpy().copy(), "pages": pages}
+        self.mark("kv_scatter_8192")
+        t = self.run(lambda i: llmk.kv_scatter(sc[i]["src"], sc[i]["pool"], sc[i]["table"], 0, T,
+                                               ps, kvdim, check_indices=False), R)
+        self.kernels["kv_scatter_8192"] = kernel_entry(
+            "kv_scatter 8192 rows (prefill)", nb, t, self.traffic.get("kv_scatter_8192"),
+            {"sets": R, "pages": pages})
+        del sc
+        self.free()
+
+        n, max_pages = 256, 128
+        lens = rng.integers(1, max_pages * ps + 1, n)
+        npages = (lens + ps - 1) // ps
+        total = int(npages.sum())
+        perm = rng.permutation(total).astype(np.int32)
+        tables = np.zeros((n, max_pages), np.int32)
+        off = 0
+        for b, pb in enumerate(npages):
+            tables[b, :pb] = perm[off:off + pb]
+            off += pb
+        pool = wl.poisoned(total * ps * kvdim, self.dev)
+        dtab = torch.from_numpy(tables).to(self.dev)
+        dpos = torch.from_numpy((lens - 1).astype(np.int32)).to(self.dev)
+        R = 16
+        srcs = [wl.normal_f16((n, kvdim), g, self.dev) for _ in range(R)]
+        self.cpu_inputs["kv_scatter_batch_256"] = {
+            "src": srcs[0].cpu().numpy().view(np.uint16).copy(), "tables": tables,
+            "pos": (lens - 1).astype(np.int32), "total": total}
+        self.mark("kv_scatter_batch_256")
+        t = self.run(lambda i: llmk.kv_scatter_batch(srcs[i], pool, dtab, dpos, n, max_pages, ps,
+                                                     kvdim, check_indices=False), R)
+        self.kernels["kv_scatter_batch_256"] = kernel_entry(
+            "kv_scatter_batch 256 sequences", wl.bytes_kv_scatter_batch(n, kvdim), t,
+            self.traffic.get("kv_scatter_batch_256"),
+            {"sets": R, "note": "one launch, 0.5 MB: bound by the launch, not the bytes"})
+        del srcs, pool
+        self.free()
+
     # ------------------------------------------------------------------ config 5
     def config5(self, table=None):
         """The 16-layer non-GEMM decode pass over 256 sequences: two input sets (642 MB between
@@ -1067,6 +1150,46 @@ class Bench:
             out["embedding_8192"] = figure("embedding_8192", wl.bytes_embedding(8192, H), mk5,
                                            f"gathers of 8192 rows from [128256,2048] (cycling "
                                            f"through {len(d['ids'])} id sets)")
+        d = self.cpu_inputs.get("residual_add_8192x2048")
+        if d:
+            r = d["residual"].copy()
+
+            def mk6(th):  # in place, as the GPU runs it
+                return lambda: lib.or_residual_add_mt(P(r), P(d["x"]), P(r), r.size, th)
+            out["residual_add_8192x2048"] = figure(
+                "residual_add_8192x2048", wl.bytes_residual_add(r.size), mk6,
+                "in-place [8192,2048] residual adds")
+            o = np.empty_like(d["x"])
+
+            def mk7(th):
+                return lambda: lib.or_rmsnorm_mt(P(d["x"]), P(d["w"]), P(o), 8192, H, eps, th)
+            out["rmsnorm_8192x2048"] = figure("rmsnorm_8192x2048", wl.bytes_rmsnorm(8192, H), mk7,
+                                              "[8192,2048] RMSNorm passes")
+        d = self.cpu_inputs.get("kv_scatter_8192")
+        if d:
+            kvdim = wl.N_KV * wl.HEAD_DIM
+            pool = np.full(d["pages"] * wl.PAGE * kvdim, 0x7F7F, np.uint16)
+
+            def mk8(th):
+                return lambda: lib.or_kv_scatter_mt(P(d["src"]), P(pool), P(d["table"], i32), 0,
+                                                    8192, wl.PAGE, kvdim, th)
+            out["kv_scatter_8192"] = figure("kv_scatter_8192",
+                                            wl.bytes_kv_scatter(8192, kvdim, wl.PAGE), mk8,
+                                            "prefill scatters of 8192 rows")
+        d = self.cpu_inputs.get("kv_scatter_batch_256")
+        if d:
+            kvdim = wl.N_KV * wl.HEAD_DIM
+            pool = np.full(d["total"] * wl.PAGE * kvdim, 0x7F7F, np.uint16)
+
+            def mk9(th):  # 256 rows: the scalar function, one core
+                return lambda: lib.or_kv_scatter_batch(P(d["src"]), P(pool), P(d["tables"], i32),
+                                                       P(d["pos"], i32), 256, 128, wl.PAGE, kvdim)
+            c = figure("kv_scatter_batch_256", wl.bytes_kv_scatter_batch(256, kvdim), mk9,
+                       "decode scatters of 256 rows")
+            if c:
+                c["cores"] = 1
+                c["sample"] += " (single-threaded: 256 rows)"
+            out["kv_scatter_batch_256"] = c
         h = self.cpu_inputs.get("decode_pass_16x256")
         if h is not None:
             out["decode_pass_16x256"] = figure(
@@ -1297,6 +1420,8 @@ def main() -> int:
         b.attention()
     if allk:
         b.argmax()
+    if allk or what == "rows":
+        b.other_rows()
     if what in ("all", "step"):
         b.decode_step(256)
     if what in ("all", "step8"):

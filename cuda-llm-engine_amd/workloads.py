@@ -56,6 +56,19 @@ def bytes_rmsnorm(rows: int, hidden: int) -> int:
     return 2 * rows * hidden * 2 + hidden * 2
 
 
+def bytes_residual_add(n: int) -> int:
+    return 3 * n * 2  # a and b read, out written
+
+
+def bytes_kv_scatter(T: int, kvdim: int, page_size: int = PAGE) -> int:
+    # source rows read, pool rows written, one table entry per page touched
+    return 2 * T * kvdim * 2 + (T + page_size - 1) // page_size * 4
+
+
+def bytes_kv_scatter_batch(n: int, kvdim: int) -> int:
+    return n * (2 * kvdim * 2 + 4 + 4)  # the row read and written; its position and table entry
+
+
 def bytes_rope(T: int, nh: int, nkv: int, hd: int) -> int:
     return 2 * T * (nh + nkv) * hd * 2 + T * 4 + hd // 2 * 4  # q, k in place; positions; table
 

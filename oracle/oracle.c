@@ -379,6 +379,17 @@ static void* run_job(void* p) {
     case 4:
       linear_cols(j->i0, j->i1, j->o0, j->a, j->b, j->c, j->r0, j->r1);
       break;
+    case 5:
+      or_residual_add(j->i0 + j->r0, j->i1 + j->r0, j->o0 + j->r0, j->r1 - j->r0);
+      break;
+    case 6:
+      or_rmsnorm(j->i0 + j->r0 * (size_t)j->a, j->i1, j->o0 + j->r0 * (size_t)j->a,
+                 (int)(j->r1 - j->r0), j->a, j->eps);
+      break;
+    case 7: /* rows r0..r1 of the source are positions start_pos + r0 .. */
+      or_kv_scatter(j->i0 + j->r0 * (size_t)j->c, j->o0, j->ids, j->a + (int)j->r0,
+                    (int)(j->r1 - j->r0), j->b, j->c);
+      break;
   }
   return NULL;
 }
@@ -444,6 +455,41 @@ void or_embedding_lookup_mt(const uint16_t* table, const int32_t* ids, uint16_t*
   j.o0 = out;
   j.a = hidden;
   run_split(j, (size_t)n_tokens, nthreads);
+}
+
+void or_residual_add_mt(const uint16_t* a, const uint16_t* b, uint16_t* out, size_t n,
+                        int nthreads) {
+  job_t j = {0};
+  j.kind = 5;
+  j.i0 = a;
+  j.i1 = b;
+  j.o0 = out;
+  run_split(j, n, nthreads);
+}
+
+void or_rmsnorm_mt(const uint16_t* x, const uint16_t* w, uint16_t* out, int n_rows, int hidden,
+                   float eps, int nthreads) {
+  job_t j = {0};
+  j.kind = 6;
+  j.i0 = x;
+  j.i1 = w;
+  j.o0 = out;
+  j.a = hidden;
+  j.eps = eps;
+  run_split(j, (size_t)n_rows, nthreads);
+}
+
+void or_kv_scatter_mt(const uint16_t* src, uint16_t* pool, const int32_t* block_table,
+                      int start_pos, int T, int page_size, int kvdim, int nthreads) {
+  job_t j = {0};
+  j.kind = 7;
+  j.i0 = src;
+  j.o0 = pool;
+  j.ids = block_table;
+  j.a = start_pos;
+  j.b = page_size;
+  j.c = kvdim;
+  run_split(j, (size_t)T, nthreads);
 }
 
 /* ------------------------------------------------------------------------------------------ */

@@ -375,6 +375,20 @@ def test_threaded_variants_equal_single_thread(orc):
     ids = rng.integers(0, 100, 53).astype(np.int32)
     assert np.array_equal(orc.embedding_lookup(table, ids, 256),
                           orc.embedding_lookup(table, ids, 256, threads=3))
+    a, b = normal_f16(rng, 100_003), normal_f16(rng, 100_003)
+    assert np.array_equal(orc.residual_add(a, b), orc.residual_add(a, b, threads=6))
+    assert np.array_equal(orc.rmsnorm(x, w, rows, hidden, EPS),
+                          orc.rmsnorm(x, w, rows, hidden, EPS, threads=5))
+    # prefill scatter of 45 rows from position 7 over a shuffled 4-page table
+    kvdim, ps = 512, 16
+    src = normal_f16(rng, (45, kvdim))
+    tab = rng.permutation(4).astype(np.int32)
+    pa = np.full(4 * ps * kvdim, 0x7F7F, np.uint16)
+    pb = pa.copy()
+    orc.kv_scatter(src, pa, tab, 7, 45, ps, kvdim)
+    orc.kv_scatter(src, pb, tab, 7, 45, ps, kvdim, threads=4)
+    assert np.array_equal(pa, pb)
+    assert (pa != 0x7F7F).sum() > 0
 
 
 # --------------------------------------------------------------------------------------------
