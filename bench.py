@@ -133,6 +133,12 @@ SECTION_ROWS = 12
 # grid choices at the benchmark shapes.
 PROFILE_SHAPES = [
     ("add_rmsnorm_8192x2048", "headline", "k_rmsnorm_waveILi4ELb1ELb1E", 8192 * 64, 134221824),
+    # 8192 blocks of 256 threads over 2,097,152 vectors; 4 rows (waves) per block from 4096 rows;
+    # the scatters: one row per wave, 4 waves per block from 4096 rows
+    ("residual_add_8192x2048", "residual_add", "k_residual_add_vec", 8192 * 256, 100663296),
+    ("rmsnorm_8192x2048", "rmsnorm_8192", "k_rmsnorm_waveILi4ELb0ELb1E", 2048 * 256, 67112960),
+    ("kv_scatter_8192", "kv_scatter_8192", "k_kv_scatterILb0ELi1E", 2048 * 256, 16779264),
+    ("kv_scatter_batch_256", "kv_scatter_batch_256", "k_kv_scatterILb1ELi1E", 256 * 64, 526336),
     ("rmsnorm_16x2048", "rmsnorm_16", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
     # 8 tokens per block, 10 vector tasks per thread (40 heads x 8 vectors x 8 tokens / 256)
     ("rope_8192", "rope_8192", "k_rope_vec", 1024 * 256, 83918976),
