@@ -159,12 +159,14 @@ __device__ __forceinline__ void load_chunk(Chunk<KVW>& c, const f16* __restrict_
   const size_t base = chunk_base<KVW>(pages, pos0, row0, row_halves);
   const f16* kb = k_pool + base;
   const f16* vb = v_pool + base;
+  // All K rows first: the scores wait only for them, and the softmax runs while V arrives
+  // (memory waits are counted in issue order).
 #pragma unroll
-  for (int r = 0; r < Chunk<KVW>::ROWS; ++r) {
-    const uint32_t off = lane_off + (uint32_t)r * row_step;
-    c.k[r] = ld16_stream(kb + off);
-    c.v[r] = ld16_stream(vb + off);
-  }
+  for (int r = 0; r < Chunk<KVW>::ROWS; ++r)
+    c.k[r] = ld16_stream(kb + lane_off + (uint32_t)r * row_step);
+#pragma unroll
+  for (int r = 0; r < Chunk<KVW>::ROWS; ++r)
+    c.v[r] = ld16_stream(vb + lane_off + (uint32_t)r * row_step);
 }
 
 // Folds a loaded chunk into the online softmax. FULL: every position of the chunk is cached;
