@@ -57,7 +57,8 @@ SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_819
             "pass_stage_add_rmsnorm", "pass_stage_rope_kv_scatter", "pass_stage_swiglu",
             "pass_floor_stages", "attention_256", "attention_16x2048", "attention_sweep",
             "argmax", "step_256", "step_8", "sched", "probe_sweep", "probe_kernels", "copy_1GiB",
-            "residual_add", "rmsnorm_8192", "kv_scatter_8192", "kv_scatter_batch_256", "end"]
+            "residual_add", "rmsnorm_8192", "kv_scatter_8192", "kv_scatter_batch_256",
+            "pass2_graph", "pass2_layers", "end"]
 
 # Launch shapes (blocks, threads) of the 16-layer pass at 256 sequences, from the launchers'
 # grid rules: the embedding and add+RMSNorm take one 64-thread wave per row below 4096 rows
@@ -750,6 +751,54 @@ class Bench:
         del srcs, pool
         self.free()
 
+    def config5_two_norms(self, table=None):
+        """Config 5 with both of the real layer's add + RMSNorm pairs per layer (the second one
+        between the RoPE + K/V scatter and the SwiGLU): 65 launches op by op, or 16 with one
+        launch per layer; two input sets replayed alternately from HIP graphs."""
+        wl, llmk, torch = self.wl, self.llmk, self.torch
+        if table is None:
+            table = wl.embedding_table(seed=wl.SEED_BASE + 40)
+        L, n = wl.LAYERS, 256
+        ps = [wl.decode_pass_inputs(self.inv, table=table, seed=wl.SEED_BASE + 62 + 100 * i,
+                                    two_norms=True) for i in range(2)]
+        dps = [llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables,
+                                      p.positions, p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
+                                      n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
+                                      page_size=wl.PAGE, max_pages=p.max_pages, eps=wl.EPS)
+               for p in ps]
+
+        def capture(fn):
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                fn()
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn()
+            return g
+
+        steps, warm = max(20, self.K // 4), max(5, self.W // 4)
+        nb = wl.bytes_decode_pass(n, L, two_norms=True)
+        graphs = [capture(dp.run) for dp in dps]
+        self.mark("pass2_graph")
+        t = self.run(lambda i: graphs[i].replay(), 2, steps, warm)
+        self.kernels["decode_pass_16x256_two_norms"] = kernel_entry(
+            "decode pass, both norms per layer (graph)", nb, t, None,
+            {"launches": 1 + 4 * L, "layers": L, "seqs": n, "sets": 2,
+             "note": "the real layer's two add + RMSNorm pairs per layer (config 5 lists one); "
+                     "388 MB per pass"})
+        del graphs
+        lgraphs = [capture(dp.run_layers) for dp in dps]
+        self.mark("pass2_layers")
+        t = self.run(lambda i: lgraphs[i].replay(), 2, steps, warm)
+        self.kernels["decode_pass_16x256_two_norms_layers"] = kernel_entry(
+            "decode pass, both norms, one launch per layer", nb, t, None,
+            {"launches": L, "layers": L, "seqs": n, "sets": 2})
+        del lgraphs, dps, ps
+        self.free()
+
     # ------------------------------------------------------------------ config 5
     def config5(self, table=None):
         """The 16-layer non-GEMM decode pass over 256 sequences: two input sets (642 MB between
@@ -1421,6 +1470,7 @@ def main() -> int:
     table = b.config4b() if allk or what == "configs" else None
     if allk or what in ("configs", "pass"):
         b.config5(table)
+        b.config5_two_norms(table)
     del table
     if allk or what == "attn":
         b.attention()

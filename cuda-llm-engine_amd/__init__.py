@@ -68,6 +68,8 @@ class DecodePass(ctypes.Structure):
         ("k_pool", ctypes.POINTER(_vp)), ("v_pool", ctypes.POINTER(_vp)),
         ("gate", ctypes.POINTER(_vp)), ("up", ctypes.POINTER(_vp)),
         ("act", ctypes.POINTER(_vp)),
+        ("x2", ctypes.POINTER(_vp)), ("norm_w2", ctypes.POINTER(_vp)),
+        ("normed2", ctypes.POINTER(_vp)),
     ]
 
 
@@ -508,7 +510,9 @@ class DecodeNonGemmPass:
     layer add+RMSNorm, fused RoPE + K/V scatter, and SwiGLU (``llmk_decode_nongemm_pass``).
 
     ``layers`` is a list of dicts with the per-layer tensors x, norm_w, normed, q, k, v,
-    k_pool, v_pool, gate, up, act. The descriptor (host pointer arrays) is built once; ``run``
+    k_pool, v_pool, gate, up, act; with x2, norm_w2 and normed2 in every layer as well, each
+    layer also runs its second add + RMSNorm (after the RoPE + K/V scatter, before the SwiGLU),
+    as the reference layer does. The descriptor (host pointer arrays) is built once; ``run``
     enqueues the whole pass on one stream and can be captured into a CUDA/HIP graph.
     """
 
@@ -536,6 +540,11 @@ class DecodeNonGemmPass:
         need = {"x": n * hidden, "norm_w": hidden, "normed": n * hidden,
                 "q": n * n_heads * head_dim, "k": n * kvdim, "v": n * kvdim, "k_pool": 0,
                 "v_pool": 0, "gate": n * inter, "up": n * inter, "act": n * inter}
+        second = [all(k in layer for k in ("x2", "norm_w2", "normed2")) for layer in layers]
+        if any(second) and not all(second):
+            _fail(fn, "x2, norm_w2 and normed2 go in every layer or in none")
+        if layers and all(second):
+            need.update({"x2": n * hidden, "norm_w2": hidden, "normed2": n * hidden})
         self._arrays = {}
         for key, cnt in need.items():
             arr = (_vp * max(1, len(layers)))()

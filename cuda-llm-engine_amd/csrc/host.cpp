@@ -59,7 +59,8 @@ extern "C" int llmk_compute_rope_inv_freq(int head_dim, double theta, double fac
 
 // One non-GEMM decode pass, launched op by op on one stream (capturable into a HIP graph).
 // Mirrors the per-layer order of ref: engine/batched.cu:112-115 with the layer body of
-// engine/batched.cu:51-71 reduced to its non-GEMM operations.
+// engine/batched.cu:51-71 reduced to its non-GEMM operations: one add + RMSNorm per layer, or
+// both of the layer's (x2 set), the second between the RoPE + K/V scatter and the SwiGLU.
 extern "C" int llmk_decode_nongemm_pass(const llmk_decode_pass* p, void* stream) {
   if (!p) return LLMK_ERR_INVALID_VALUE;
   if (p->n_seqs < 0 || p->n_layers < 0 || p->hidden <= 0 || p->inter <= 0)
@@ -67,6 +68,9 @@ extern "C" int llmk_decode_nongemm_pass(const llmk_decode_pass* p, void* stream)
   if (p->n_seqs == 0) return LLMK_OK;
   if (p->n_layers > 0 && (!p->x || !p->norm_w || !p->normed || !p->q || !p->k || !p->v ||
                           !p->k_pool || !p->v_pool || !p->gate || !p->up || !p->act))
+    return LLMK_ERR_INVALID_VALUE;
+  const bool two_norms = p->x2 || p->norm_w2 || p->normed2;
+  if (two_norms && p->n_layers > 0 && (!p->x2 || !p->norm_w2 || !p->normed2))
     return LLMK_ERR_INVALID_VALUE;
   const int n = p->n_seqs;
   int st = llmk_embedding_lookup(p->embed_table, p->token_ids, p->residual, n, p->hidden, stream);
@@ -79,6 +83,11 @@ extern "C" int llmk_decode_nongemm_pass(const llmk_decode_pass* p, void* stream)
                                     p->block_tables, p->positions, p->inv_freq, n, p->max_pages,
                                     p->page_size, p->n_heads, p->n_kv_heads, p->head_dim, stream);
     if (st != LLMK_OK) return st;
+    if (two_norms) {
+      st = llmk_add_rmsnorm(p->residual, p->x2[l], p->norm_w2[l], p->normed2[l], n, p->hidden,
+                            p->eps, stream);
+      if (st != LLMK_OK) return st;
+    }
     st = llmk_swiglu(p->gate[l], p->up[l], p->act[l], (size_t)n * p->inter, stream);
     if (st != LLMK_OK) return st;
   }

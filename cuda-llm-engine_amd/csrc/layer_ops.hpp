@@ -16,6 +16,34 @@ namespace llmk {
 // residual update; r_in and r_out are the same row except when r_in is an embedding row), and
 // the norm is taken of it. FULL: vpr == 64 * VPL, every lane owns exactly VPL vectors.
 // ---------------------------------------------------------------------------------------------
+// The normalised row of the lane's vectors h (fp16, already rounded) times the weights wv,
+// stored to out.
+template <int VPL, bool FULL>
+__device__ __forceinline__ void norm_store(const f16x8 (&h)[VPL], const f16x8 (&wv)[VPL],
+                                           f16* out, int vpr, float hidden_f, float eps,
+                                           int lane) {
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = (float)h[k][j];
+      ss = ss + f * f;
+    }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / __builtin_sqrtf(ss / hidden_f + eps);
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int v = lane + 64 * k;
+    if (FULL || v < vpr) {
+      f16x8 a;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = (f16)((float)h[k][j] * inv);
+      st16_stream(out + 8 * v, as_u4(wv[k] * a));
+    }
+  }
+}
+
 template <int VPL, bool FUSED, bool FULL>
 __device__ __forceinline__ void rmsnorm_row(const f16* x, const f16* r_in, f16* r_out,
                                             const f16* __restrict__ w, f16* out, int vpr,
@@ -41,26 +69,40 @@ __device__ __forceinline__ void rmsnorm_row(const f16* x, const f16* r_in, f16* 
       if (owned(v)) st16_stream(r_out + 8 * v, as_u4(h[k]));
     }
   }
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < VPL; ++k)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float f = (float)h[k][j];
-      ss = ss + f * f;
-    }
-  ss = wave_sum(ss);
-  const float inv = 1.0f / __builtin_sqrtf(ss / hidden_f + eps);
+  norm_store<VPL, FULL>(h, wv, out, vpr, hidden_f, eps, lane);
+}
+
+// Both of a layer's add + RMSNorm pairs on one row: h = r_in + x, out = norm(h) * w, then
+// h = h + x2, r_out = h, out2 = norm(h) * w2. The same bits as two rmsnorm_row<VPL, true, FULL>
+// calls with the residual stored and re-read in between; here it stays in registers.
+template <int VPL, bool FULL>
+__device__ __forceinline__ void rmsnorm_row2(const f16* x, const f16* x2, const f16* r_in,
+                                             f16* r_out, const f16* __restrict__ w,
+                                             const f16* __restrict__ w2, f16* out, f16* out2,
+                                             int vpr, float hidden_f, float eps, int lane) {
+  auto owned = [&](int v) { return FULL || v < vpr; };
+  f16x8 h[VPL], wv[VPL], x2v[VPL], wv2[VPL];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int v = lane + 64 * k;
     if (owned(v)) {
-      f16x8 a;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) a[j] = (f16)((float)h[k][j] * inv);
-      st16_stream(out + 8 * v, as_u4(wv[k] * a));
+      h[k] = as_h8(ld16_stream(x + 8 * v));
+      x2v[k] = as_h8(ld16_stream(x2 + 8 * v));
+      h[k] = as_h8(ld16_stream(r_in + 8 * v)) + h[k];
+      wv[k] = as_h8(ld16(w + 8 * v));
+      wv2[k] = as_h8(ld16(w2 + 8 * v));
+    } else {
+      h[k] = x2v[k] = wv[k] = wv2[k] = (f16x8)(f16)0;
     }
   }
+  norm_store<VPL, FULL>(h, wv, out, vpr, hidden_f, eps, lane);
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    h[k] = h[k] + x2v[k];
+    const int v = lane + 64 * k;
+    if (owned(v)) st16_stream(r_out + 8 * v, as_u4(h[k]));
+  }
+  norm_store<VPL, FULL>(h, wv2, out2, vpr, hidden_f, eps, lane);
 }
 
 // ---------------------------------------------------------------------------------------------

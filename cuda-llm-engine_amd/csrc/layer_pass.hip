@@ -7,9 +7,11 @@
 // of one-wave blocks: blocks [0, n) take the add + RMSNorm rows, blocks [n, 2n) the RoPE + K/V
 // scatter of one token each, the rest the SwiGLU chunks. The first layer's norm rows read their
 // residual input straight from the embedding table (the gather fused into the add), so the
-// pass is n_layers launches. Every block runs the same body as the stand-alone kernel
-// (layer_ops.hpp), so the results are the same bits. Blocks are dispatched in index order: the
-// latency-bound norm and RoPE blocks go first, the SwiGLU stream fills the rest.
+// pass is n_layers launches. With the layer's second add + RMSNorm (x2 set), a norm block runs
+// both on its row, the residual kept in registers between them. Every block runs the same body
+// as the stand-alone kernel (layer_ops.hpp), so the results are the same bits. Blocks are
+// dispatched in index order: the latency-bound norm and RoPE blocks go first, the SwiGLU stream
+// fills the rest.
 #include "layer_ops.hpp"
 
 namespace llmk {
@@ -18,6 +20,8 @@ namespace {
 struct LayerArgs {
   const f16 *x, *norm_w;
   f16* normed;
+  const f16 *x2, *norm_w2;  // the second add + RMSNorm (NORM2)
+  f16* normed2;
   f16* q;
   const f16 *k, *v;
   f16 *k_pool, *v_pool;
@@ -36,15 +40,20 @@ struct LayerArgs {
 
 constexpr int kWave = 64;
 
-template <int VPL, bool EMBED, int TASKS>
+template <int VPL, bool EMBED, int TASKS, bool NORM2>
 __global__ void __launch_bounds__(kWave) k_layer_pass(LayerArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int b = blockIdx.x;
   if (b < a.n) {
     const size_t base = (size_t)b * a.vpr * 8;
     const f16* r_in = EMBED ? a.embed + (size_t)a.ids[b] * a.vpr * 8 : a.residual + base;
-    rmsnorm_row<VPL, true, true>(a.x + base, r_in, a.residual + base, a.norm_w, a.normed + base,
-                                 a.vpr, a.hidden_f, a.eps, threadIdx.x);
+    if (NORM2)
+      rmsnorm_row2<VPL, true>(a.x + base, a.x2 + base, r_in, a.residual + base, a.norm_w,
+                              a.norm_w2, a.normed + base, a.normed2 + base, a.vpr, a.hidden_f,
+                              a.eps, threadIdx.x);
+    else
+      rmsnorm_row<VPL, true, true>(a.x + base, r_in, a.residual + base, a.norm_w,
+                                   a.normed + base, a.vpr, a.hidden_f, a.eps, threadIdx.x);
   } else if (b < 2 * a.n) {
     rope_tile<4, TASKS, true, false>(b - a.n, kWave, smem, a.q, a.k, a.v, a.k_pool, a.v_pool,
                                      a.tables, a.pos, a.inv_freq, a.n, a.nh, a.nkv, 1,
@@ -60,24 +69,25 @@ __global__ void __launch_bounds__(kWave) k_layer_pass(LayerArgs a) {
   }
 }
 
-template <int VPL, bool EMBED>
+template <int VPL, bool EMBED, bool NORM2>
 int launch_layer(const LayerArgs& a, int tasks, unsigned blocks, size_t lds, hipStream_t s) {
+  const dim3 g(blocks), t(kWave);
   switch (tasks) {
-    case 6: return launch(k_layer_pass<VPL, EMBED, 6>, dim3(blocks), dim3(kWave), lds, s, a);
-    case 8: return launch(k_layer_pass<VPL, EMBED, 8>, dim3(blocks), dim3(kWave), lds, s, a);
-    case 12: return launch(k_layer_pass<VPL, EMBED, 12>, dim3(blocks), dim3(kWave), lds, s, a);
-    default: return launch(k_layer_pass<VPL, EMBED, 16>, dim3(blocks), dim3(kWave), lds, s, a);
+    case 6: return launch(k_layer_pass<VPL, EMBED, 6, NORM2>, g, t, lds, s, a);
+    case 8: return launch(k_layer_pass<VPL, EMBED, 8, NORM2>, g, t, lds, s, a);
+    case 12: return launch(k_layer_pass<VPL, EMBED, 12, NORM2>, g, t, lds, s, a);
+    default: return launch(k_layer_pass<VPL, EMBED, 16, NORM2>, g, t, lds, s, a);
   }
 }
 
-template <bool EMBED>
+template <bool EMBED, bool NORM2>
 int launch_layer_vpl(const LayerArgs& a, int tasks, unsigned blocks, size_t lds, hipStream_t s) {
   switch (a.vpr / 64) {
-    case 1: return launch_layer<1, EMBED>(a, tasks, blocks, lds, s);
-    case 2: return launch_layer<2, EMBED>(a, tasks, blocks, lds, s);
-    case 4: return launch_layer<4, EMBED>(a, tasks, blocks, lds, s);
-    case 8: return launch_layer<8, EMBED>(a, tasks, blocks, lds, s);
-    default: return launch_layer<16, EMBED>(a, tasks, blocks, lds, s);
+    case 1: return launch_layer<1, EMBED, NORM2>(a, tasks, blocks, lds, s);
+    case 2: return launch_layer<2, EMBED, NORM2>(a, tasks, blocks, lds, s);
+    case 4: return launch_layer<4, EMBED, NORM2>(a, tasks, blocks, lds, s);
+    case 8: return launch_layer<8, EMBED, NORM2>(a, tasks, blocks, lds, s);
+    default: return launch_layer<16, EMBED, NORM2>(a, tasks, blocks, lds, s);
   }
 }
 
@@ -100,6 +110,8 @@ extern "C" int llmk_decode_nongemm_pass_layers(const llmk_decode_pass* p, void* 
       !p->v_pool || !p->gate || !p->up || !p->act || !p->block_tables || !p->positions ||
       !p->inv_freq)
     return LLMK_ERR_INVALID_VALUE;
+  const bool two_norms = p->x2 || p->norm_w2 || p->normed2;
+  if (two_norms && (!p->x2 || !p->norm_w2 || !p->normed2)) return LLMK_ERR_INVALID_VALUE;
   // Shapes this launch implements; others take llmk_decode_nongemm_pass.
   const int per_tok = (p->n_heads + 2 * p->n_kv_heads) * 8;  // 16-byte vectors per token
   const int tasks = (per_tok + kWave - 1) / kWave;
@@ -119,6 +131,10 @@ extern "C" int llmk_decode_nongemm_pass_layers(const llmk_decode_pass* p, void* 
         !al(p->k[l]) || !al(p->v[l]) || !al(p->k_pool[l]) || !al(p->v_pool[l]) ||
         !al(p->gate[l]) || !al(p->up[l]) || !al(p->act[l]))
       return LLMK_ERR_ALIGNMENT;
+    if (two_norms) {
+      if (!p->x2[l] || !p->norm_w2[l] || !p->normed2[l]) return LLMK_ERR_INVALID_VALUE;
+      if (!al(p->x2[l]) || !al(p->norm_w2[l]) || !al(p->normed2[l])) return LLMK_ERR_ALIGNMENT;
+    }
   }
   LayerArgs a;
   a.residual = reinterpret_cast<f16*>(p->residual);
@@ -156,8 +172,16 @@ extern "C" int llmk_decode_nongemm_pass_layers(const llmk_decode_pass* p, void* 
     a.gate = reinterpret_cast<const f16*>(p->gate[l]);
     a.up = reinterpret_cast<const f16*>(p->up[l]);
     a.act = reinterpret_cast<f16*>(p->act[l]);
-    const int st = l == 0 ? launch_layer_vpl<true>(a, ptasks, blocks, lds, s)
-                          : launch_layer_vpl<false>(a, ptasks, blocks, lds, s);
+    a.x2 = two_norms ? reinterpret_cast<const f16*>(p->x2[l]) : nullptr;
+    a.norm_w2 = two_norms ? reinterpret_cast<const f16*>(p->norm_w2[l]) : nullptr;
+    a.normed2 = two_norms ? reinterpret_cast<f16*>(p->normed2[l]) : nullptr;
+    int st;
+    if (two_norms)
+      st = l == 0 ? launch_layer_vpl<true, true>(a, ptasks, blocks, lds, s)
+                  : launch_layer_vpl<false, true>(a, ptasks, blocks, lds, s);
+    else
+      st = l == 0 ? launch_layer_vpl<true, false>(a, ptasks, blocks, lds, s)
+                  : launch_layer_vpl<false, false>(a, ptasks, blocks, lds, s);
     if (st != LLMK_OK) return st;
   }
   return LLMK_OK;

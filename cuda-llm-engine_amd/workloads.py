@@ -88,8 +88,8 @@ def bytes_rope_kv_scatter(n: int, nh: int, nkv: int, hd: int) -> int:
     # sequence's row address needs, the rotation table
 
 
-def bytes_decode_pass(n: int, layers: int) -> int:
-    per_layer = (bytes_add_rmsnorm(n, HIDDEN)
+def bytes_decode_pass(n: int, layers: int, two_norms: bool = False) -> int:
+    per_layer = ((2 if two_norms else 1) * bytes_add_rmsnorm(n, HIDDEN)
                  + bytes_rope_kv_scatter(n, N_HEADS, N_KV, HEAD_DIM)
                  + bytes_swiglu(n * INTER))
     return bytes_embedding(n, HIDDEN) + layers * per_layer
@@ -244,9 +244,11 @@ class DecodePassInputs:
 
 def decode_pass_inputs(inv_freq: torch.Tensor, n=256, layers=LAYERS, max_pages=128,
                        table=None, seed=SEED_BASE + 5, device="cuda", hidden=HIDDEN,
-                       n_heads=N_HEADS, n_kv=N_KV, inter=INTER,
-                       vocab=VOCAB) -> DecodePassInputs:
-    """Config 5's inputs (by default); the model dimensions can be changed for shape tests."""
+                       n_heads=N_HEADS, n_kv=N_KV, inter=INTER, vocab=VOCAB,
+                       two_norms=False) -> DecodePassInputs:
+    """Config 5's inputs (by default); the model dimensions can be changed for shape tests.
+    two_norms: each layer also gets x2, norm_w2 and normed2 for its second add + RMSNorm (the
+    real layer's two; config 5 lists one)."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(1, max_pages * PAGE + 1, n)
     npages = (lens + PAGE - 1) // PAGE
@@ -276,6 +278,11 @@ def decode_pass_inputs(inv_freq: torch.Tensor, n=256, layers=LAYERS, max_pages=1
             gate=normal_f16((n, inter), g, device),
             up=normal_f16((n, inter), g, device),
             act=torch.empty((n, inter), dtype=torch.float16, device=device)))
+        if two_norms:
+            per_layer[-1].update(
+                x2=normal_f16((n, hidden), g, device),
+                norm_w2=normal_f16((hidden,), g, device, 1.0, 0.1),
+                normed2=torch.empty((n, hidden), dtype=torch.float16, device=device))
     return DecodePassInputs(
         n=n, layers=layers, max_pages=max_pages, total_pages=total, lens=lens,
         tables_host=tables, table=table, token_ids=ids,

@@ -249,6 +249,12 @@ typedef struct llmk_decode_pass {
   const uint16_t* const* gate;     /* per layer [n_seqs, inter] */
   const uint16_t* const* up;       /* per layer [n_seqs, inter] */
   uint16_t* const* act;            /* per layer [n_seqs, inter] */
+  /* Optional, all NULL or all set: each layer's second add + RMSNorm, as the reference layer
+   * adds the attention output and normalises for the MLP (engine/batched.cu:64-66); it runs
+   * after the RoPE + K/V scatter and before the SwiGLU. */
+  const uint16_t* const* x2;       /* per layer [n_seqs, hidden]: added into residual */
+  const uint16_t* const* norm_w2;  /* per layer [hidden] */
+  uint16_t* const* normed2;        /* per layer [n_seqs, hidden] */
 } llmk_decode_pass;
 
 LLMK_API int llmk_decode_nongemm_pass(const llmk_decode_pass* pass, void* stream);

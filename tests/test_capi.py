@@ -142,6 +142,36 @@ def test_argument_validation_without_launch(llmk):
     assert L.llmk_argmax_rows(None, FAKE, 4, 100, None) == E.LLMK_ERR_INVALID_VALUE
 
 
+def test_decode_pass_descriptor_validation_without_launch(llmk):
+    """The decode-pass descriptor: the second add + RMSNorm is all or nothing, in both passes,
+    refused before any launch (no pointer here is dereferenced)."""
+    import ctypes
+    L, E = llmk._lib, llmk
+    arr = (ctypes.c_void_p * 1)(FAKE)
+    parr = ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p))
+
+    def desc(**second):
+        d = E.DecodePass()
+        d.n_seqs, d.n_layers, d.hidden, d.n_heads, d.n_kv_heads = 4, 1, 2048, 32, 8
+        d.head_dim, d.inter, d.page_size, d.max_pages, d.eps = 64, 8192, 16, 8, 1e-5
+        for f in ("embed_table", "token_ids", "residual", "block_tables", "positions",
+                  "inv_freq"):
+            setattr(d, f, FAKE)
+        for f in ("x", "norm_w", "normed", "q", "k", "v", "k_pool", "v_pool", "gate", "up",
+                  "act"):
+            setattr(d, f, parr)
+        for f, v in second.items():
+            setattr(d, f, v)
+        return ctypes.byref(d)
+
+    for fn in (L.llmk_decode_nongemm_pass, L.llmk_decode_nongemm_pass_layers):
+        assert fn(desc(x2=parr), None) == E.LLMK_ERR_INVALID_VALUE
+        assert fn(desc(x2=parr, norm_w2=parr), None) == E.LLMK_ERR_INVALID_VALUE
+        assert fn(desc(normed2=parr), None) == E.LLMK_ERR_INVALID_VALUE
+        assert fn(None, None) == E.LLMK_ERR_INVALID_VALUE
+    assert ctypes.sizeof(E.DecodePass) == 10 * 4 + 6 * 8 + 14 * 8
+
+
 def test_split_count_rule_and_its_default(llmk):
     """choose_num_splits restates the reference's rule (kernels/attention_decode_fast.cuh:22-29);
     the Python default equals LLMK_ATTN_TARGET_BLOCKS of the C header."""

@@ -111,6 +111,9 @@ def _check_decode_pass(orc, wl, p, inv_h, expected_residual_in):
         for pool in (kp, vp):
             changed = (pool.view(torch.int16) != poison).any(dim=1)
             assert int(changed.sum()) == n, f"layer {l}: rows outside the addressed slots changed"
+        if "x2" in L:  # the layer's second add + RMSNorm, after the scatter
+            normed2 = orc.add_rmsnorm(res, host(L["x2"]), host(L["norm_w2"]), n, hidden, EPS)
+            assert_tol(orc.compare(host(L["normed2"]), normed2), 0.99, f"layer {l} normed2")
         act = orc.swiglu(host(L["gate"]), host(L["up"]), threads=THREADS)
         assert_tol(orc.compare(host(L["act"]), act), 0.995, f"layer {l} act")
     return res
@@ -131,6 +134,28 @@ def test_config5_decode_pass_16_layers_256_seqs(llmk, orc, wl, inv):
     assert np.array_equal(emb, host(p.table).reshape(-1, wl.HIDDEN)[ids])
     final = _check_decode_pass(orc, wl, p, inv[0], emb)
     assert np.array_equal(host(p.residual), final), "residual chain must be bit-exact"
+
+
+def test_decode_pass_with_both_norms_per_layer(llmk, orc, wl, inv):
+    """The real layer's two add + RMSNorm pairs (the reference adds the attention output and
+    normalises again before the MLP, engine/batched.cu:64-66): 4 layers x 256 sequences against
+    the oracle layer by layer, the residual chain bit-exact; then the one-launch-per-layer pass
+    on the same inputs gives every output's bits."""
+    kw = dict(layers=4, seed=wl.SEED_BASE + 61, two_norms=True)
+    p = wl.decode_pass_inputs(inv[1], **kw)
+    for L in p.per_layer:
+        L["q_in"] = L["q"].clone()
+    dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables, p.positions,
+                                p.inv_freq, p.per_layer, n_heads=wl.N_HEADS,
+                                n_kv_heads=wl.N_KV, head_dim=wl.HEAD_DIM, inter=wl.INTER,
+                                page_size=wl.PAGE, max_pages=p.max_pages, eps=EPS)
+    dp.run()
+    torch.cuda.synchronize()
+    emb = host(p.table.index_select(0, p.token_ids.long()))
+    final = _check_decode_pass(orc, wl, p, inv[0], emb)
+    assert np.array_equal(host(p.residual), final), "residual chain must be bit-exact"
+    (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **kw)
+    _same_pass_bits(pa, da, pb, db)
 
 
 def test_decode_pass_hip_graph_replays(llmk, orc, wl, inv):
@@ -205,14 +230,17 @@ def _same_pass_bits(pa, da, pb, db):
     for L in pb.per_layer:
         L["act"].fill_(float("nan"))
         L["normed"].fill_(float("nan"))
+        if "normed2" in L:
+            L["normed2"].fill_(float("nan"))
     pb.residual.fill_(float("nan"))
     da.run()
     db.run_layers()
     torch.cuda.synchronize()
     assert torch.equal(pa.residual.view(torch.int16), pb.residual.view(torch.int16))
     for l, (A, B) in enumerate(zip(pa.per_layer, pb.per_layer)):
-        for key in ("normed", "q", "act", "k_pool", "v_pool"):
-            assert torch.equal(A[key].view(torch.int16), B[key].view(torch.int16)), (l, key)
+        for key in ("normed", "q", "act", "k_pool", "v_pool", "normed2"):
+            if key in A:
+                assert torch.equal(A[key].view(torch.int16), B[key].view(torch.int16)), (l, key)
 
 
 @pytest.mark.parametrize("shape", [dict(n=64, layers=3, max_pages=32, seed=0x5EED0000 + 56),
@@ -236,14 +264,19 @@ PASS_MODELS = [(512, 8, 2, 1376), (1024, 16, 4, 2816), (2048, 48, 8, 5632),
                (4096, 64, 8, 11008), (8192, 112, 8, 8192), (2048, 64, 16, 4096)]
 
 
-@pytest.mark.parametrize("model", PASS_MODELS, ids=lambda m: "h%d_q%d_kv%d" % m[:3])
-def test_decode_pass_one_launch_per_layer_across_model_shapes(llmk, wl, inv, model):
+@pytest.mark.parametrize("model,two_norms",
+                         [(m, False) for m in PASS_MODELS] + [(PASS_MODELS[1], True),
+                                                              (PASS_MODELS[4], True)],
+                         ids=lambda v: ("h%d_q%d_kv%d" % v[:3]) if isinstance(v, tuple)
+                         else ("two_norms" if v else "one_norm"))
+def test_decode_pass_one_launch_per_layer_across_model_shapes(llmk, wl, inv, model, two_norms):
     """The one-launch-per-layer pass against the op-by-op pass (each of whose kernels is checked
     against the oracle on its own) at other model dimensions than config 5's: 29 sequences
-    (a partial last SwiGLU chunk), 2 layers, bit for bit."""
+    (a partial last SwiGLU chunk), 2 layers, bit for bit; with both of a layer's norms at two of
+    the row widths."""
     hidden, nh, nkv, inter = model
     kw = dict(n=29, layers=2, max_pages=8, seed=0x5EED0000 + 58, hidden=hidden, n_heads=nh,
-              n_kv=nkv, inter=inter, vocab=1000)
+              n_kv=nkv, inter=inter, vocab=1000, two_norms=two_norms)
     (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **kw)
     _same_pass_bits(pa, da, pb, db)
 
