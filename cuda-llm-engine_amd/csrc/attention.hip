@@ -844,23 +844,23 @@ k_attn_merge_many(const float* __restrict__ part_o, const float2* __restrict__ p
   }
 }
 
-// Blocks of k_attn_balanced<KVW> that fit on the device at once (cached per device).
-template <int KVW>
-int resident_blocks() {
+// The page-balanced grid's block count: one 4-wave block per CU (cached per device). Two
+// resident blocks per CU, twice the waves, measured slower: the runs are half as long, so
+// sequences split into twice the pieces and each block switches segments twice as often
+// (same box: 256 of U[1, 2048] 100.1 -> 98.9 us with one block per CU, 64 x 2048
+// 50.3 -> 48.5, 256 x 2048 172.6 -> 168.4; one 8-wave block per CU 101.2 / 50.2 / 170.9).
+int balanced_blocks() {
   static int cache[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   const int known = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
   if (known > 0) return known;
-  int cus = 0, per_cu = 0;
+  int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &per_cu, reinterpret_cast<const void*>(k_attn_balanced<KVW>), kThreads, 0) !=
-          hipSuccess)
+      cus <= 0)
     return 0;
-  const int n = cus * (per_cu > 0 ? per_cu : 1);
-  __atomic_store_n(&cache[dev], n, __ATOMIC_RELAXED);
-  return n;
+  __atomic_store_n(&cache[dev], cus, __ATOMIC_RELAXED);
+  return cus;
 }
 
 struct AttnArgs {
@@ -905,7 +905,7 @@ int attn_launch(const AttnArgs& a, hipStream_t s) {
   const bool short_runs = a.part_o && a.num_splits >= 3 && pps <= kShortRunPages &&
                           (long long)a.n_seq * groups <= kSplitGridPairs;
   if (a.num_splits >= 3 && a.part_o && !short_runs) {
-    int blocks = resident_blocks<KVW>() / groups;
+    int blocks = balanced_blocks() / groups;
     if (blocks < 1) blocks = 1;
     int st = launch(k_attn_balanced<KVW>, dim3((unsigned)blocks, (unsigned)groups), dim3(kThreads),
                     0, s, a.lens, a.tables, a.n_seq, a.max_pages, a.n_heads, a.n_kv_heads,

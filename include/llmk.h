@@ -133,7 +133,7 @@ LLMK_API int llmk_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const ui
 /* Default target block count of choose_num_splits (llmk.hpp) for MI355X. The reference's
  * default, 64, was fitted to a 20-SM laptop GPU (ref: kernels/attention_decode_fast.cuh:20-22).
  * Here num_splits only caps how many pieces a sequence may be cut into (libllmk balances the
- * pages of the whole batch over one resident round of blocks), so the default asks for as many
+ * pages of the whole batch over one block per CU), so the default asks for as many
  * as the rule allows: 32 for batches up to 256 sequences of 8 kv heads. */
 #define LLMK_ATTN_TARGET_BLOCKS 65536
 
