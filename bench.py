@@ -146,8 +146,8 @@ PROFILE_SHAPES = [
     ("swiglu_8192x8192", "swiglu_8192", "k_swiglu_vecILi1E", 131072 * 64, 402653184),
     ("embedding_8192", "embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
     ("copy_1GiB", "copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),
-    # 512 blocks: two resident blocks of 256 threads on each of the 256 CUs (191 VGPRs).
-    ("attention_decode_256", "attention_256", "k_attn_balancedILi8E", 512 * 256,
+    # 256 blocks: one block of 256 threads on each of the 256 CUs.
+    ("attention_decode_256", "attention_256", "k_attn_balancedILi8E", 256 * 256,
      ATTN_BYTES_256),
     ("attention_merge_256", "attention_256", "k_attn_merge", 256 * 256, None),
     # 16 sequences take the sequence-split grid (32 splits of 4 pages, 16 blocks per split).
