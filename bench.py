@@ -162,7 +162,7 @@ PROFILE_SHAPES = [
      3147904),
     ("decode:swiglu_256x8192", "pass_graph", "k_swiglu_vecILi1E", 4096 * 64, 12582912),
     # the pass with one launch per layer: 256 norm rows, 256 RoPE tokens, 4096 SwiGLU chunks
-    ("decode_layers:layer_256", "pass_layers", "k_layer_passILi4ELb0ELi6E|k_layer_pass<4, false, 6>",
+    ("decode_layers:layer_256", "pass_layers", "k_layer_passILi4ELb0ELi6ELb0E|k_layer_pass<4, false, 6, false>",
      4608 * 64, 4198400 + 3147904 + 12582912),
 ]
 
@@ -293,6 +293,10 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
     print("#")
     summarize_pass(tagged, "pass_graph", "k_embedding", 49)
     summarize_pass(tagged, "pass_layers", "k_layer_passILi4ELb1E|k_layer_pass<4, true", 16)
+    print("#")
+    summarize_pass(tagged, "pass2_graph", "k_embedding", 65)
+    print("#")
+    summarize_pass(tagged, "pass2_layers", "k_layer_passILi4ELb1E|k_layer_pass<4, true", 16)
     return 1 if missing else 0
 
 
