@@ -266,13 +266,23 @@ struct MergeLds {
   float m[NP][HEADS], l[NP][HEADS];
 };
 
-// The lane's 8 dims of the 4 query heads that share its kv head (kv head kvg * 8 + octet % KVW)
-// for sequence `seq`.
+// The kv head of the lane's octet: kvg * 8 + octet % KVW. A last kv group with fewer than 8
+// heads (n_kv_heads not a multiple of 8: rows of 3, 5, 6, 7, 12, ... heads) gives its spare
+// octets the group's last head, so that they read inside the row and the query; their results
+// are never stored (every store checks the query head against n_heads).
+template <int KVW>
+__device__ __forceinline__ int lane_kv_head(int kvg, int n_kv_heads) {
+  const int kvh = kvg * 8 + ((threadIdx.x & 63) >> 3) % KVW;
+  return KVW == 8 && kvh >= n_kv_heads ? n_kv_heads - 1 : kvh;
+}
+
+// The lane's 8 dims of the 4 query heads that share its kv head (lane_kv_head) for sequence
+// `seq`.
 template <int KVW>
 __device__ __forceinline__ void load_query(u32x4 (&qv)[kGroup], const f16* __restrict__ q,
                                            int seq, int kvg, int n_heads) {
   const int lane = threadIdx.x & 63;
-  const int kvh = kvg * 8 + (lane >> 3) % KVW;
+  const int kvh = lane_kv_head<KVW>(kvg, n_heads / kGroup);
 #pragma unroll
   for (int i = 0; i < kGroup; ++i)
     qv[i] = ld16(q + ((size_t)seq * n_heads + kvh * kGroup + i) * kHeadDim + (lane & 7) * 8);
@@ -302,9 +312,12 @@ __device__ __forceinline__ void attend_segment(const u32x4 (&qv)[kGroup],
   const int octet = lane >> 3, d8 = lane & 7;
   const int slot = octet / KVW, kvl = octet % KVW;
   const size_t row_halves = (size_t)n_kv_heads * kHeadDim;
-  // Lane's offset inside a row read: this kv group's 8 heads, then 16 bytes per lane (for
-  // KVW < 8 the lanes run on into the next PPL - 1 rows, which are contiguous within a page).
-  const uint32_t lane_off = (uint32_t)(kvg * 8 * kHeadDim + lane * 8);
+  // Lane's offset inside a row read: its kv head (lane_kv_head), then 16 bytes per lane of the
+  // octet (for KVW < 8 the lanes run on into the next PPL - 1 rows, which are contiguous within
+  // a page).
+  const uint32_t lane_off =
+      KVW == 8 ? (uint32_t)(lane_kv_head<KVW>(kvg, n_kv_heads) * kHeadDim + d8 * 8)
+               : (uint32_t)(kvg * 8 * kHeadDim + lane * 8);
   const uint32_t row_step = (uint32_t)(PPL * row_halves);
 
   SoftmaxState st;
@@ -900,7 +913,7 @@ int split_launch(const AttnArgs& a, int groups, int pps, hipStream_t s) {
 
 template <int KVW>
 int attn_launch(const AttnArgs& a, hipStream_t s) {
-  const int groups = a.n_kv_heads >= 8 ? a.n_kv_heads / 8 : 1;
+  const int groups = KVW == 8 ? (a.n_kv_heads + 7) / 8 : 1;
   const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;  // pages per split
   const bool short_runs = a.part_o && a.num_splits >= 3 && pps <= kShortRunPages &&
                           (long long)a.n_seq * groups <= kSplitGridPairs;
@@ -987,12 +1000,13 @@ static int run_attention(const uint16_t* q, const uint16_t* k_pool, const uint16
   a.n_kv_heads = n_kv_heads;
   a.num_splits = num_splits;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (n_kv_heads % 8 == 0) return attn_launch<8>(a, s);
+  // Rows of 1, 2 or 4 kv heads put several positions in one row read; any other count takes
+  // kv groups of 8, the last one partly idle when the count is not a multiple of 8.
   switch (n_kv_heads) {
     case 4: return attn_launch<4>(a, s);
     case 2: return attn_launch<2>(a, s);
     case 1: return attn_launch<1>(a, s);
-    default: return LLMK_ERR_UNSUPPORTED;  // a row of 3, 5, 6 or 7 kv heads
+    default: return attn_launch<8>(a, s);
   }
 }
 

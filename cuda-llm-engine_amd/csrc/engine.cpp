@@ -126,8 +126,6 @@ int valid_config(const llmk_model_config& c) {
   if (c.head_dim != 64 || c.n_heads != 4 * c.n_kv_heads || c.hidden % 8 != 0 ||
       c.inter % 8 != 0)
     return LLMK_ERR_SHAPE;
-  if (c.n_kv_heads % 8 != 0 && c.n_kv_heads != 1 && c.n_kv_heads != 2 && c.n_kv_heads != 4)
-    return LLMK_ERR_UNSUPPORTED;
   return LLMK_OK;
 }
 

@@ -111,7 +111,7 @@ def test_argument_validation_without_launch(llmk):
     assert A(*[FAKE] * 7, 4, 8, 32, 32, 8, 64, 4, None) == E.LLMK_ERR_SHAPE
     assert A(*[FAKE] * 7, 4, 8, 16, 32, 8, 128, 4, None) == E.LLMK_ERR_SHAPE
     assert A(*[FAKE] * 7, 4, 8, 16, 24, 8, 64, 4, None) == E.LLMK_ERR_SHAPE
-    assert A(*[FAKE] * 7, 4, 8, 16, 12, 3, 64, 4, None) == E.LLMK_ERR_UNSUPPORTED
+    assert A(*[FAKE] * 7, 65536, 8, 16, 32, 8, 64, 4, None) == E.LLMK_ERR_UNSUPPORTED
     assert A(*[FAKE] * 7, 4, 8, 16, 32, 8, 64, 0, None) == E.LLMK_ERR_INVALID_VALUE
     assert A(*[FAKE] * 6, None, 4, 8, 16, 32, 8, 64, 2, None) == E.LLMK_ERR_INVALID_VALUE
     assert A(MIS, *[FAKE] * 6, 4, 8, 16, 32, 8, 64, 2, None) == E.LLMK_ERR_ALIGNMENT

@@ -86,10 +86,11 @@ def test_results_do_not_depend_much_on_the_split_count(llmk, orc, reference_case
         assert_tol(orc.compare(d.run(llmk, splits), one), EXACT_FLOOR, f"splits {splits} vs 1")
 
 
-@pytest.mark.parametrize("nkv", [1, 2, 4, 16])
+@pytest.mark.parametrize("nkv", [1, 2, 3, 4, 5, 6, 7, 12, 16])
 def test_other_kv_head_counts(llmk, orc, nkv):
     """The reference accepts any n_kv with 4 query heads each; rows of 1, 2 or 4 kv heads put
-    several positions in one 1 KiB row read, 16 kv heads take two blocks per split."""
+    several positions in one 1 KiB row read, 16 kv heads take two blocks per split, and a count
+    that is not a multiple of 8 (3, 5, 6, 7, 12) leaves part of its last kv group idle."""
     c = attention_case(np.random.default_rng(nkv), (1, 7, 16, 33, 130, 500), n_heads=4 * nkv,
                        n_kv_heads=nkv)
     d = OnDevice(c)
@@ -108,10 +109,11 @@ def test_small_batch_in_short_runs(llmk, orc, reference_case, splits):
     assert_tol(cmp, EXACT_FLOOR, f"short runs, splits {splits}")
 
 
-@pytest.mark.parametrize("nkv", [1, 2, 4, 16])
+@pytest.mark.parametrize("nkv", [1, 2, 4, 6, 12, 16])
 def test_short_runs_with_other_kv_head_counts(llmk, orc, nkv):
-    """Short runs with rows of 1, 2 or 4 kv heads (several positions per row read) and with 16
-    kv heads (two kv groups): 32-page tables cut into runs of 1, 2 and 4 pages."""
+    """Short runs with rows of 1, 2 or 4 kv heads (several positions per row read), with 16
+    kv heads (two kv groups) and with 6 and 12 (a partly idle last group): 32-page tables cut
+    into runs of 1, 2 and 4 pages."""
     c = attention_case(np.random.default_rng(100 + nkv), (1, 7, 16, 33, 130, 500),
                        n_heads=4 * nkv, n_kv_heads=nkv)
     assert c["max_pages"] == 32
@@ -164,7 +166,7 @@ def test_preconditions_are_reported(llmk, reference_case):
 
     for kw, status in [(dict(page_size=32), llmk.LLMK_ERR_SHAPE),
                        (dict(n_heads=16), llmk.LLMK_ERR_SHAPE),
-                       (dict(n_kv_heads=3, n_heads=12), llmk.LLMK_ERR_UNSUPPORTED),
+                       (dict(n_kv_heads=3, n_heads=16), llmk.LLMK_ERR_SHAPE),
                        (dict(num_splits=0), llmk.LLMK_ERR_INVALID_VALUE)]:
         with pytest.raises(llmk.LlmkError) as e:
             call(**kw)

@@ -382,12 +382,16 @@ def check_logits(orc, got, got_next, exp, exp_next, what):
     assert np.array_equal(got_next, orc.argmax_rows(got, got.shape[0], got.shape[1]))
 
 
-def test_engine_matches_oracle_small_model(llmk, orc):
-    w = tiny_weights(0x5EED0230, embed_std=0.5)
+@pytest.mark.parametrize("cfg", [TINY, dict(TINY, n_heads=12, n_kv_heads=3)],
+                         ids=["1_kv_head", "3_kv_heads"])
+def test_engine_matches_oracle_small_model(llmk, orc, cfg):
+    """Prefill and decode rows through the engine against the oracle; with one kv head, and
+    with three (a count the attention runs as a partly idle group of 8)."""
+    w = tiny_weights(0x5EED0230, embed_std=0.5, cfg=cfg)
     rng = np.random.default_rng(0x5EED0231)
-    s = Session(llmk, orc, TINY, w, w, n_seqs=3, max_rows=64, max_pages=8, num_pages=30,
+    s = Session(llmk, orc, cfg, w, w, n_seqs=3, max_rows=64, max_pages=8, num_pages=30,
                 seed=0x5EED0232)
-    V = TINY["vocab"]
+    V = cfg["vocab"]
     prompts = [rng.integers(0, V, L) for L in (20, 33, 7)]
     # step 1: two prompts in one batch (53 rows); step 2: the third prompt plus two decode rows;
     # then decode steps for all three
@@ -400,33 +404,35 @@ def test_engine_matches_oracle_small_model(llmk, orc):
 
 
 WIDE = dict(TINY, hidden=512, n_heads=8, n_kv_heads=2, inter=1024, vocab=1000)
+WIDE6 = dict(WIDE, n_heads=24, n_kv_heads=6)
 
 
-@pytest.mark.parametrize("n", [1, 3, 8])
-def test_engine_fused_few_rows_pass_gives_the_bits_of_the_unfused_pass(llmk, orc, n):
+@pytest.mark.parametrize("n,cfg", [(1, WIDE), (3, WIDE), (8, WIDE), (3, WIDE6)],
+                         ids=["1", "3", "8", "3_six_kv_heads"])
+def test_engine_fused_few_rows_pass_gives_the_bits_of_the_unfused_pass(llmk, orc, n, cfg):
     """A decode step of n <= 8 rows runs the fused few-rows projections (norms, RoPE + scatter,
     SwiGLU and residual adds inside the projections). It must reproduce the unfused pass bit for
     bit: logits, greedy tokens, residual stream and every pool of every layer."""
-    w = tiny_weights(0x5EED0250, embed_std=0.5, cfg=WIDE)
+    w = tiny_weights(0x5EED0250, embed_std=0.5, cfg=cfg)
     num_pages, max_pages = 64, 8
-    e = make_engine(llmk, WIDE, w, 16, max_pages, num_pages)
+    e = make_engine(llmk, cfg, w, 16, max_pages, num_pages)
     rng = np.random.default_rng(0x5EED0251 + n)
     tables = rng.permutation(num_pages).astype(np.int32)[:n * max_pages].reshape(n, max_pages)
     pos = rng.integers(0, max_pages * 16, n).astype(np.int32)
-    tok = rng.integers(0, WIDE["vocab"], n).astype(np.int32)
-    kvdim = WIDE["n_kv_heads"] * WIDE["head_dim"]
+    tok = rng.integers(0, cfg["vocab"], n).astype(np.int32)
+    kvdim = cfg["n_kv_heads"] * cfg["head_dim"]
     fill = torch.randn(num_pages * 16 * kvdim, device=DEV).half()
 
     def run(fuse):
         e.set_option(llmk.ENGINE_FUSE_FEW_ROWS, fuse)
-        for l in range(WIDE["n_layers"]):
+        for l in range(cfg["n_layers"]):
             for which in (llmk.BUF_K_POOL, llmk.BUF_V_POOL):
                 e.write_pool(which, l, fill)
         e.set_rows(tok, pos, tables)
         e.forward(n)
         torch.cuda.synchronize()
         got = [e.logits(n), e.next_tokens(n), e.residual(n)]
-        got += [e.pool(wh, l) for l in range(WIDE["n_layers"])
+        got += [e.pool(wh, l) for l in range(cfg["n_layers"])
                 for wh in (llmk.BUF_K_POOL, llmk.BUF_V_POOL)]
         return [t.clone().view(torch.int16) if t.dtype == torch.float16 else t.clone()
                 for t in got]
