@@ -150,8 +150,8 @@ LLMK_API size_t llmk_attention_decode_fast_workspace_floats(int n_seq, int n_hea
  * page_size + j % page_size, kv head h / (n_heads / n_kv_heads). Layouts: q and out
  * [n_seq, n_heads, head_dim]; pools [num_pages, page_size, n_kv_heads, head_dim]; block_tables
  * [n_seq, max_pages]. Requires page_size 16, head_dim 64, n_heads == 4 * n_kv_heads (the
- * reference's preconditions: LLMK_ERR_SHAPE otherwise) and n_kv_heads a multiple of 8 or one of
- * 1, 2, 4 (LLMK_ERR_UNSUPPORTED otherwise). Each sequence is cut into at most num_splits runs of
+ * reference's preconditions: LLMK_ERR_SHAPE otherwise) and n_seq <= 65535 (the reference's grid
+ * limit too; LLMK_ERR_UNSUPPORTED otherwise). Each sequence is cut into at most num_splits runs of
  * ceil(max_pages / num_splits) pages; with more than one run the partial results go through
  * `workspace` (llmk_attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits) floats,
  * 16-byte aligned; may be NULL when num_splits == 1) and a second launch merges them. A
