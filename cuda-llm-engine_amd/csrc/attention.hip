@@ -266,13 +266,13 @@ struct MergeLds {
   float m[NP][HEADS], l[NP][HEADS];
 };
 
-// The kv head of the lane's octet: kvg * 8 + octet % KVW. A last kv group with fewer than 8
-// heads (n_kv_heads not a multiple of 8: rows of 3, 5, 6, 7, 12, ... heads) gives its spare
-// octets the group's last head, so that they read inside the row and the query; their results
-// are never stored (every store checks the query head against n_heads).
+// The kv head of the lane's octet: kvg * KVW + octet % KVW (kv group kvg holds KVW heads). A
+// last group of 8 with fewer heads (n_kv_heads not a multiple of 8: rows of 3, 5, 6, 7, 12, ...
+// heads) gives its spare octets the group's last head, so that they read inside the row and the
+// query; their results are never stored (every store checks the query head against n_heads).
 template <int KVW>
 __device__ __forceinline__ int lane_kv_head(int kvg, int n_kv_heads) {
-  const int kvh = kvg * 8 + ((threadIdx.x & 63) >> 3) % KVW;
+  const int kvh = kvg * KVW + ((threadIdx.x & 63) >> 3) % KVW;
   return KVW == 8 && kvh >= n_kv_heads ? n_kv_heads - 1 : kvh;
 }
 
@@ -312,12 +312,12 @@ __device__ __forceinline__ void attend_segment(const u32x4 (&qv)[kGroup],
   const int octet = lane >> 3, d8 = lane & 7;
   const int slot = octet / KVW, kvl = octet % KVW;
   const size_t row_halves = (size_t)n_kv_heads * kHeadDim;
-  // Lane's offset inside a row read: its kv head (lane_kv_head), then 16 bytes per lane of the
-  // octet (for KVW < 8 the lanes run on into the next PPL - 1 rows, which are contiguous within
-  // a page).
+  // Lane's offset inside a row read: its position's row (for KVW < 8 a row read spans PPL
+  // consecutive positions of a page, one per slot), its kv head (lane_kv_head), then 16 bytes
+  // per lane of the octet. With KVW == n_kv_heads the row read is one contiguous run; with fewer
+  // (a row cut into n_kv_heads / KVW kv groups) it is PPL pieces of KVW * 128 bytes.
   const uint32_t lane_off =
-      KVW == 8 ? (uint32_t)(lane_kv_head<KVW>(kvg, n_kv_heads) * kHeadDim + d8 * 8)
-               : (uint32_t)(kvg * 8 * kHeadDim + lane * 8);
+      (uint32_t)(slot * row_halves + lane_kv_head<KVW>(kvg, n_kv_heads) * kHeadDim + d8 * 8);
   const uint32_t row_step = (uint32_t)(PPL * row_halves);
 
   SoftmaxState st;
@@ -913,7 +913,7 @@ int split_launch(const AttnArgs& a, int groups, int pps, hipStream_t s) {
 
 template <int KVW>
 int attn_launch(const AttnArgs& a, hipStream_t s) {
-  const int groups = KVW == 8 ? (a.n_kv_heads + 7) / 8 : 1;
+  const int groups = KVW == 8 ? (a.n_kv_heads + 7) / 8 : a.n_kv_heads / KVW;
   const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;  // pages per split
   const bool short_runs = a.part_o && a.num_splits >= 3 && pps <= kShortRunPages &&
                           (long long)a.n_seq * groups <= kSplitGridPairs;
@@ -979,6 +979,25 @@ static int check_attention(const uint16_t* q, const uint16_t* k_pool, const uint
   return -1;
 }
 
+// Kv heads per kv group (one grid row of blocks each). Rows of 1, 2 or 4 kv heads put several
+// positions in one row read. Any other count takes groups of 8 (the last one partly idle when
+// the count is not a multiple of 8), except for very small batches. At most 8 (sequence, kv
+// group) pairs cut their rows into narrower groups: 4 or 2 heads of 2 or 4 positions per row
+// read. That gives more blocks, each with a shorter chain of dependent loads. Same box, 2048
+// positions, 8 kv heads: 1 sequence 10.31 -> 8.25 us with groups of 2, 2 sequences 10.44 ->
+// 8.71, 4 sequences 10.67 -> 9.67 with groups of 4. At 8 or more sequences, groups of 8 are as
+// fast or faster; groups of 1 lose everywhere.
+static int kv_group_width(int n_seq, int n_kv_heads) {
+  if (n_kv_heads == 1 || n_kv_heads == 2 || n_kv_heads == 4) {
+    int w = n_kv_heads;
+    while (w > 2 && (long long)n_seq * (n_kv_heads / (w / 2)) <= 8) w /= 2;
+    return w;
+  }
+  for (int w = 2; w <= 4; w *= 2)  // the narrowest width whose pairs fit
+    if (n_kv_heads % w == 0 && (long long)n_seq * (n_kv_heads / w) <= 8) return w;
+  return 8;
+}
+
 static int run_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                          const int32_t* block_tables, const int32_t* seq_lens, uint16_t* out,
                          float* workspace, int n_seq, int max_pages, int n_heads, int n_kv_heads,
@@ -1000,9 +1019,7 @@ static int run_attention(const uint16_t* q, const uint16_t* k_pool, const uint16
   a.n_kv_heads = n_kv_heads;
   a.num_splits = num_splits;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Rows of 1, 2 or 4 kv heads put several positions in one row read; any other count takes
-  // kv groups of 8, the last one partly idle when the count is not a multiple of 8.
-  switch (n_kv_heads) {
+  switch (kv_group_width(n_seq, n_kv_heads)) {
     case 4: return attn_launch<4>(a, s);
     case 2: return attn_launch<2>(a, s);
     case 1: return attn_launch<1>(a, s);

@@ -123,6 +123,23 @@ def test_short_runs_with_other_kv_head_counts(llmk, orc, nkv):
         assert_tol(orc.compare(d.run(llmk, splits), ref), EXACT_FLOOR, f"n_kv {nkv} splits {splits}")
 
 
+@pytest.mark.parametrize("lens,nkv", [((2048,), 8), ((2048, 17), 8), ((33, 2048, 1, 500), 8),
+                                      ((2048,), 16), ((700, 1500), 16), ((2048,), 12),
+                                      ((130, 2048), 12), ((2048,), 6), ((1, 2047), 4)])
+def test_very_small_batches_take_narrower_kv_groups(llmk, orc, lens, nkv):
+    """At most 8 (sequence, kv group) pairs cut each row into narrower kv groups (2 or 4 heads, a
+    row read spanning 4 or 2 positions): 1-4 sequences with 4, 6, 8, 12 and 16 kv heads, at the
+    split counts the short-run grid (32), the page-balanced grid (3) and a single split (1)
+    take."""
+    c = attention_case(np.random.default_rng(300 + nkv + len(lens)), lens, n_heads=4 * nkv,
+                       n_kv_heads=nkv)
+    d = OnDevice(c)
+    ref = oracle_out(orc, c)
+    for splits in (1, 3, 32):
+        assert_tol(orc.compare(d.run(llmk, splits), ref), EXACT_FLOOR,
+                   f"lens {lens} n_kv {nkv} splits {splits}")
+
+
 def test_empty_sequences_give_nan_and_leave_the_rest_intact(llmk, orc):
     c = attention_case(np.random.default_rng(5), (0, 5, -3, 40))
     d = OnDevice(c)
