@@ -974,7 +974,7 @@ static int check_attention(const uint16_t* q, const uint16_t* k_pool, const uint
       n_heads != kGroup * n_kv_heads)
     return LLMK_ERR_SHAPE;
   if (n_seq < 0 || max_pages <= 0 || num_splits <= 0) return LLMK_ERR_INVALID_VALUE;
-  if (n_seq > 65535 || n_kv_heads / 8 > 65535) return LLMK_ERR_UNSUPPORTED;
+  if (n_seq > 65535 || (n_kv_heads + 7) / 8 > 65535) return LLMK_ERR_UNSUPPORTED;
   if (!q || !k_pool || !v_pool || !block_tables || !seq_lens || !out)
     return LLMK_ERR_INVALID_VALUE;
   if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
