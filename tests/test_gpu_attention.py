@@ -140,6 +140,21 @@ def test_very_small_batches_take_narrower_kv_groups(llmk, orc, lens, nkv):
                    f"lens {lens} n_kv {nkv} splits {splits}")
 
 
+@pytest.mark.parametrize("n_seq", [1024, 1025, 3000])
+def test_many_sequences(llmk, orc, n_seq):
+    """Batches around and past the 1024 sequences (4 tiles of 256 threads) whose page counts the
+    page-balanced kernel keeps in registers; past it, each block re-reads the lengths tile by tile
+    while it looks for its first sequence. Short contexts (1-48 positions), so blocks cross
+    dozens of sequences each; one split (the sequence-split grid), 3 and 32 (page-balanced)."""
+    rng = np.random.default_rng(7000 + n_seq)
+    c = attention_case(rng, rng.integers(1, 49, n_seq))
+    d = OnDevice(c)
+    ref = oracle_out(orc, c)
+    for splits in (1, 3, 32):
+        assert_tol(orc.compare(d.run(llmk, splits), ref), EXACT_FLOOR,
+                   f"{n_seq} sequences, splits {splits}")
+
+
 def test_empty_sequences_give_nan_and_leave_the_rest_intact(llmk, orc):
     c = attention_case(np.random.default_rng(5), (0, 5, -3, 40))
     d = OnDevice(c)
