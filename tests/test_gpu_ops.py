@@ -182,6 +182,8 @@ def test_add_rmsnorm_equals_residual_add_then_rmsnorm(llmk):
 # --------------------------------------------------------------------------------------------
 ROPE_SHAPES = [  # (T, n_heads, n_kv_heads, head_dim)
     (1, 32, 8, 64), (5, 32, 8, 64), (1023, 32, 8, 64),
+    (1500, 32, 8, 64),             # 2 tokens per block
+    (3001, 32, 8, 64),             # 4 tokens per block, partial last block
     (4100, 32, 8, 64),             # 8 tokens per block, partial last block
     (17, 16, 4, 128), (9, 8, 2, 256), (33, 4, 1, 32), (6, 3, 1, 16),
     (7, 32, 0, 64), (5, 0, 8, 64),
