@@ -86,11 +86,11 @@ def run_cpp(llmk, reqs, max_running, num_pages, max_pages, order=None):
     return outs, stats, times, fake, pages
 
 
-def run_oracle(reqs, max_running, num_pages, max_pages, order=None):
+def run_oracle(reqs, max_running, num_pages, max_pages, order=None, **rule):
     fake = FakePagedModel(num_pages, max_pages)
     free = list(range(num_pages - 1, -1, -1)) if order is None else list(order)
     outs, stats, free_end = oracle.scheduler_run(reqs, max_running, max_pages, P, free,
-                                                 fake.prefill, fake.decode)
+                                                 fake.prefill, fake.decode, **rule)
     return outs, stats, fake, free_end
 
 
@@ -137,7 +137,8 @@ def test_outputs_are_each_requests_own_and_pages_all_return(llmk, max_running):
 def test_schedule_matches_the_reference_loop(llmk, max_running, num_pages):
     """Same model calls, in the same order, as the restatement of the reference's loop -- also
     under page pressure (9 or 12 pages for prompts of up to 60 tokens plus 11 new ones), where
-    admission waits on the pages running requests may still take."""
+    admission waits until the free pages, less those the admitted requests are still owed,
+    hold the next request's quota."""
     rng = np.random.default_rng(0x5EED0310 + max_running + num_pages)
     reqs = workload(rng, 20, spacing=1)
     max_pages = 8
@@ -150,6 +151,25 @@ def test_schedule_matches_the_reference_loop(llmk, max_running, num_pages):
         assert stats[k] == o_stats[k], k
     assert stats["mean_batch"] == pytest.approx(o_stats["mean_batch"])
     assert pages.num_free() == num_pages and len(o_free) == num_pages
+
+
+def test_a_strict_admission_rule_is_caught(llmk):
+    """A restatement that admits only when the spare pages exceed the quota (> for >=) makes
+    other model calls than the library under page pressure, so the comparison above would catch
+    that mistake; the correct restatement matches on the same cases."""
+    caught = 0
+    for seed in range(6):
+        rng = np.random.default_rng(0x5EED0330 + seed)
+        reqs = workload(rng, 20, spacing=1)
+        num_pages, max_pages = 9, 8
+        order = rng.permutation(num_pages).astype(np.int32)
+        _, stats, _, fake, _ = run_cpp(llmk, reqs, 4, num_pages, max_pages, order)
+        _, o_stats, o_fake, _ = run_oracle(reqs, 4, num_pages, max_pages, order)
+        assert fake.calls == o_fake.calls, seed
+        _, m_stats, m_fake, _ = run_oracle(reqs, 4, num_pages, max_pages, order,
+                                           fits=lambda spare, quota: spare > quota)
+        caught += m_fake.calls != fake.calls
+    assert caught >= 3, f"the strict rule changed the calls in only {caught} of 6 workloads"
 
 
 def test_batching_raises_throughput_in_model_calls(llmk):
