@@ -540,8 +540,9 @@ class DecodeNonGemmPass:
         need = {"x": n * hidden, "norm_w": hidden, "normed": n * hidden,
                 "q": n * n_heads * head_dim, "k": n * kvdim, "v": n * kvdim, "k_pool": 0,
                 "v_pool": 0, "gate": n * inter, "up": n * inter, "act": n * inter}
-        second = [all(k in layer for k in ("x2", "norm_w2", "normed2")) for layer in layers]
-        if any(second) and not all(second):
+        present = [sum(k in layer for k in ("x2", "norm_w2", "normed2")) for layer in layers]
+        second = [c == 3 for c in present]
+        if any(c not in (0, 3) for c in present) or (any(second) and not all(second)):
             _fail(fn, "x2, norm_w2 and normed2 go in every layer or in none")
         if layers and all(second):
             need.update({"x2": n * hidden, "norm_w2": hidden, "normed2": n * hidden})

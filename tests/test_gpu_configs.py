@@ -156,6 +156,19 @@ def test_decode_pass_with_both_norms_per_layer(llmk, orc, wl, inv):
     assert np.array_equal(host(p.residual), final), "residual chain must be bit-exact"
     (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **kw)
     _same_pass_bits(pa, da, pb, db)
+    # The second pair goes in every layer or in none: a layer with only some of its tensors,
+    # or layers that disagree, are refused before anything runs.
+    partial = [dict(L) for L in p.per_layer]
+    del partial[2]["normed2"]
+    mixed = [dict(L) for L in p.per_layer]
+    for key in ("x2", "norm_w2", "normed2"):
+        del mixed[0][key]
+    for layers in (partial, mixed):
+        with pytest.raises(llmk.LlmkError):
+            llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables, p.positions,
+                                   p.inv_freq, layers, n_heads=wl.N_HEADS, n_kv_heads=wl.N_KV,
+                                   head_dim=wl.HEAD_DIM, inter=wl.INTER, page_size=wl.PAGE,
+                                   max_pages=p.max_pages, eps=EPS)
 
 
 def test_decode_pass_hip_graph_replays(llmk, orc, wl, inv):
