@@ -141,8 +141,9 @@ PROFILE_SHAPES = [
     ("kv_scatter_8192", "kv_scatter_8192", "k_kv_scatterILb0ELi1E", 2048 * 256, 16779264),
     ("kv_scatter_batch_256", "kv_scatter_batch_256", "k_kv_scatterILb1ELi1E", 256 * 64, 526336),
     ("rmsnorm_16x2048", "rmsnorm_16", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
-    # 16 tokens per block, 20 vector tasks per thread (40 heads x 8 vectors x 16 tokens / 256)
-    ("rope_8192", "rope_8192", "k_rope_vec", 512 * 256, 83918976),
+    # 16 tokens per 512-thread block, 10 vector tasks per thread (40 heads x 8 vectors x 16
+    # tokens / 512)
+    ("rope_8192", "rope_8192", "k_rope_vecILi4ELi10ELb0ELb0ELi512E", 512 * 512, 83918976),
     ("swiglu_8192x8192", "swiglu_8192", "k_swiglu_vecILi1E", 131072 * 64, 402653184),
     ("embedding_8192", "embedding_8192", "k_embedding_rowsILi8E", 256 * 256, 67141632),
     ("copy_1GiB", "copy_1GiB", "k_copy", 8192 * 256, 2 * (1 << 30)),

@@ -23,20 +23,20 @@
 
 namespace llmk {
 
-// HV = 16-byte vectors per half head row (head_dim = 16 * HV); TASKS = vectors per thread. One
-// block of 256 threads per tile of tpb tokens; the tile body (layer_ops.hpp, rope_tile)
-// describes the layout and the load order.
-template <int HV, int TASKS, bool FUSED, bool STRIDED>
-__global__ void __launch_bounds__(256)
+// HV = 16-byte vectors per half head row (head_dim = 16 * HV); TASKS = vectors per thread;
+// NT = threads per block (256, or 512 for the standalone shapes below). One block per tile of
+// tpb tokens; the tile body (layer_ops.hpp, rope_tile) describes the layout and the load order.
+template <int HV, int TASKS, bool FUSED, bool STRIDED, int NT>
+__global__ void __launch_bounds__(NT)
 k_rope_vec(f16* q, const f16* k, const f16* __restrict__ v, f16* k_out, f16* v_pool,
            const int* __restrict__ tables, const int* __restrict__ pos,
            const float* __restrict__ inv_freq, int n_tokens, int nh, int nkv, int tpb,
            int max_pages, int page_size, FastDiv qdiv, FastDiv kdiv, const f16* q_src,
            int ld) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  rope_tile<HV, TASKS, FUSED, STRIDED>(blockIdx.x, blockDim.x, smem, q, k, v, k_out, v_pool,
-                                       tables, pos, inv_freq, n_tokens, nh, nkv, tpb, max_pages,
-                                       page_size, qdiv, kdiv, q_src, ld);
+  rope_tile<HV, TASKS, FUSED, STRIDED>(blockIdx.x, NT, smem, q, k, v, k_out, v_pool, tables, pos,
+                                       inv_freq, n_tokens, nh, nkv, tpb, max_pages, page_size,
+                                       qdiv, kdiv, q_src, ld);
 }
 
 // Any head_dim (even) and any alignment: one pair per thread per step, same arithmetic.
@@ -68,12 +68,39 @@ k_rope_scalar(f16* q, f16* k, const int* __restrict__ pos, const float* __restri
 }
 
 // Tokens per block: about 512 blocks for long runs, one token per block for short ones. At
-// 8192 tokens of 32 + 8 heads, 16 tokens per block (20 vectors per thread) measured 14.76-14.81
-// us against 15.03-15.11 with 8 (1024 blocks) and 17.1 with 32, same box.
+// 8192 tokens of 32 + 8 heads, 16 tokens per 256-thread block (20 vectors per thread) measured
+// 14.76-14.81 us against 15.03-15.11 with 8 (1024 blocks) and 17.1 with 32, same box.
 static int tokens_per_block(int n_tokens) {
   int tpb = 1;
   while (tpb < 16 && n_tokens / (2 * tpb) >= 512) tpb *= 2;
   return tpb;
+}
+
+// Launch shape of the standalone kernel: threads per block (*nthr) and tokens per tile (*tpb),
+// for tokens of per_tok vectors.
+//  - At most 512 tiles (a tile of at least 1024 vectors): 512-thread blocks. Two 8-wave blocks
+//    per CU then hold the whole grid in one resident round.
+//  - From 16384 tokens' worth of 320-vector tokens (Q [T, 32, 64] + K [T, 8, 64]) up: tiles of
+//    about 1280 vectors in 512-thread blocks, many rounds of them.
+//  - Otherwise 256-thread blocks of tokens_per_block tokens.
+// Same box, Q [T, 32, 64] + K [T, 8, 64], every shape bit-identical, best of two rounds (us,
+// 256-thread blocks of tokens_per_block tokens -> this shape): T = 4096 7.77 -> 7.45,
+// 8192 14.60 -> 14.13, 16384 30.86 -> 28.77, 32768 60.65 -> 54.01, 65536 121.66 -> 104.87;
+// at 12288 (768 tiles of 16) 256-thread blocks stay best, 21.4 against 22.7 with 512 threads.
+static void standalone_shape(int n_tokens, int per_tok, int* nthr, int* tpb) {
+  constexpr long long kManyVectors = 16384LL * 320;
+  *nthr = 256;
+  *tpb = tokens_per_block(n_tokens);
+  if ((long long)n_tokens * per_tok >= kManyVectors) {
+    int t = 1;
+    while (t < 16 && 2 * t * per_tok <= 1280) t *= 2;
+    if (t * per_tok >= 1024) {
+      *nthr = 512;
+      *tpb = t;
+    }
+    return;
+  }
+  if (ceil_div((size_t)n_tokens, (size_t)*tpb) <= 512 && *tpb * per_tok >= 1024) *nthr = 512;
 }
 
 template <bool FUSED, bool STRIDED = false>
@@ -83,28 +110,41 @@ static int rope_vec_launch(f16* q, const f16* k, const f16* v, f16* k_out, f16* 
                            hipStream_t stream, const f16* q_src = nullptr, int ld = 0) {
   const int hv = hd / 16;
   const int per_tok = (nh + nkv + (FUSED ? nkv : 0)) * 2 * hv;  // vectors per token
-  constexpr int kThreads = 256, kMaxTasks = 20;
-  int tpb = tokens_per_block(n_tokens);
-  while (tpb > 1 && ceil_div((size_t)tpb * per_tok, kThreads) > (unsigned)kMaxTasks) tpb /= 2;
-  const unsigned tasks = ceil_div((size_t)tpb * per_tok, kThreads);
+  constexpr int kMaxTasks = 20;
+  int nthr = 256, tpb = tokens_per_block(n_tokens);
+  if (!FUSED) standalone_shape(n_tokens, per_tok, &nthr, &tpb);
+  while (tpb > 1 && ceil_div((size_t)tpb * per_tok, nthr) > (unsigned)kMaxTasks) tpb /= 2;
+  const unsigned tasks = ceil_div((size_t)tpb * per_tok, nthr);
   if (tasks > (unsigned)kMaxTasks) return LLMK_ERR_UNSUPPORTED;
   const FastDiv qdiv = make_fastdiv((uint32_t)(nh > 0 ? nh * 2 * hv : 1));
   const FastDiv kdiv = make_fastdiv((uint32_t)(nkv > 0 ? nkv * 2 * hv : 1));
-  const dim3 grid(ceil_div((size_t)n_tokens, (size_t)tpb)), block(kThreads);
+  const dim3 grid(ceil_div((size_t)n_tokens, (size_t)tpb)), block(nthr);
   const size_t lds = (FUSED ? 8 * (size_t)tpb : 0) + (size_t)tpb * hd * sizeof(f16);
-#define LLMK_ROPE_LAUNCH(H, TK)                                                                  \
-  return launch(k_rope_vec<H, TK, FUSED, STRIDED>, grid, block, lds, stream, q, k, v, k_out,   \
-                v_pool, tables, pos, inv_freq, n_tokens, nh, nkv, tpb, max_pages, page_size,     \
-                qdiv, kdiv, q_src, ld)
-#define LLMK_ROPE_CASE(H)                \
-  case H:                                \
-    if (tasks <= 2) LLMK_ROPE_LAUNCH(H, 2);  \
-    if (tasks <= 4) LLMK_ROPE_LAUNCH(H, 4);  \
-    if (tasks <= 8) LLMK_ROPE_LAUNCH(H, 8);  \
-    if (tasks <= 10) LLMK_ROPE_LAUNCH(H, 10); \
-    if (tasks <= 12) LLMK_ROPE_LAUNCH(H, 12); \
-    if (tasks <= 16) LLMK_ROPE_LAUNCH(H, 16); \
-    LLMK_ROPE_LAUNCH(H, 20);
+#define LLMK_ROPE_LAUNCH(H, TK, NT)                                                              \
+  return launch(k_rope_vec<H, TK, FUSED, STRIDED, NT>, grid, block, lds, stream, q, k, v,      \
+                k_out, v_pool, tables, pos, inv_freq, n_tokens, nh, nkv, tpb, max_pages,         \
+                page_size, qdiv, kdiv, q_src, ld)
+  // 256 threads: 2, 4, 8, 10, 12, 16 or 20 vectors per thread. 512 threads (standalone only):
+  // the counts its shapes give exactly (3, 5, 10 for 320-vector tokens), else the next above.
+#define LLMK_ROPE_CASE(H)                                \
+  case H:                                                \
+    if constexpr (!FUSED) {                              \
+      if (nthr == 512) {                                 \
+        if (tasks <= 2) LLMK_ROPE_LAUNCH(H, 2, 512);     \
+        if (tasks <= 3) LLMK_ROPE_LAUNCH(H, 3, 512);     \
+        if (tasks <= 5) LLMK_ROPE_LAUNCH(H, 5, 512);     \
+        if (tasks <= 10) LLMK_ROPE_LAUNCH(H, 10, 512);   \
+        if (tasks <= 16) LLMK_ROPE_LAUNCH(H, 16, 512);   \
+        LLMK_ROPE_LAUNCH(H, 20, 512);                    \
+      }                                                  \
+    }                                                    \
+    if (tasks <= 2) LLMK_ROPE_LAUNCH(H, 2, 256);         \
+    if (tasks <= 4) LLMK_ROPE_LAUNCH(H, 4, 256);         \
+    if (tasks <= 8) LLMK_ROPE_LAUNCH(H, 8, 256);         \
+    if (tasks <= 10) LLMK_ROPE_LAUNCH(H, 10, 256);       \
+    if (tasks <= 12) LLMK_ROPE_LAUNCH(H, 12, 256);       \
+    if (tasks <= 16) LLMK_ROPE_LAUNCH(H, 16, 256);       \
+    LLMK_ROPE_LAUNCH(H, 20, 256);
   switch (hv) {
     LLMK_ROPE_CASE(1)
     LLMK_ROPE_CASE(2)
