@@ -182,16 +182,21 @@ def test_add_rmsnorm_equals_residual_add_then_rmsnorm(llmk):
 # --------------------------------------------------------------------------------------------
 ROPE_SHAPES = [  # (T, n_heads, n_kv_heads, head_dim)
     (1, 32, 8, 64), (5, 32, 8, 64), (1023, 32, 8, 64),
-    (1500, 32, 8, 64),             # 2 tokens per block
-    (3001, 32, 8, 64),             # 4 tokens per block, partial last block
-    (4100, 32, 8, 64),             # 8 tokens per block, partial last block
+    (1500, 32, 8, 64),             # 256 threads, 2 tokens per block
+    (3001, 32, 8, 64),             # 256 threads, 4 tokens per block, partial last block
+    (4100, 32, 8, 64),             # 256 threads, 8 tokens per block, partial last block
+    (2048, 32, 8, 64),             # 512 threads, 4 tokens (3 vectors per thread), 512 tiles
+    (4096, 32, 8, 64),             # 512 threads, 8 tokens (5 vectors per thread), 512 tiles
+    (8192, 6, 2, 64),              # 512 threads, 16 tokens of 64 vectors (2 per thread)
+    (8192, 12, 4, 256),            # 512 threads, 16 tokens of 512 vectors (16 per thread)
+    (8192, 32, 4, 128),            # 512 threads, 16 tokens of 576 vectors (18 per thread)
     (17, 16, 4, 128), (9, 8, 2, 256), (33, 4, 1, 32), (6, 3, 1, 16),
     (7, 32, 0, 64), (5, 0, 8, 64),
     (11, 4, 2, 40), (3, 2, 1, 6),  # head_dim not a multiple of 16: scalar path
-    (16385, 32, 8, 64),            # 16 tokens per block (20 vectors per thread), a last
-                                   # block of one token
-    (33001, 4, 1, 64),             # 16 tokens per block, partial last block
-    (7, 64, 8, 256),               # wide tokens: 9 vectors per thread (the 10-task kernel)
+    (16385, 32, 8, 64),            # 512 threads, 4 tokens per block (3 vectors per thread),
+                                   # a last block of one token
+    (33001, 4, 1, 64),             # 256 threads, 16 tokens per block, partial last block
+    (7, 64, 8, 256),               # wide tokens: 512 threads, 5 vectors per thread
     (2, 128, 32, 256),             # one token exceeds a block: scalar path
 ]
 
