@@ -150,7 +150,7 @@ PROFILE_SHAPES = [
     # 256 blocks: one block of 256 threads on each of the 256 CUs.
     ("attention_decode_256", "attention_256", "k_attn_balancedILi8E", 256 * 256,
      ATTN_BYTES_256),
-    ("attention_merge_256", "attention_256", "k_attn_merge", 256 * 256, None),
+    ("attention_merge_256", "attention_256", "k_attn_mergeE|k_attn_merge(", 256 * 256, None),
     # 16 sequences take the sequence-split grid (32 splits of 4 pages, 16 blocks per split).
     ("attention_decode_16x2048", "attention_16x2048", "k_attn_splitILi8ELi0E", 32 * 256 * 16,
      ATTN_BYTES_16x2048),
