@@ -395,7 +395,11 @@ def summarize_step(trace_dir, n_rows=256):
     for r in steps:
         key = (r["Kernel_Name"], _grid(r))
         agg.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    print(f"# engine decode step (Llama-3.2-1B shape, {n_rows} rows), {n_steps} graph replays")
+    print(f"# engine decode step (Llama-3.2-1B shape, {n_rows} rows), {n_steps} graph replays, "
+          "made by:")
+    print(f"#   rocprofv3 --kernel-trace --stats -f csv -d {trace_dir} -o bench -- "
+          "python3 bench.py --no-cpu")
+    print(f"#   python3 bench.py --summarize-step {trace_dir} {n_rows}")
     print("# launches/step  mean_us  us/step  grid  kernel")
     total = 0.0
     for (name, g), d in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
@@ -425,7 +429,10 @@ def summarize_sched(trace_dir, min_passes=20, top=10):
         if "k_argmax" in name:
             passes.setdefault(cur["n"], []).append(cur["k"])
             cur = None
-    print("# engine forward passes of the scheduler workload, by row count")
+    print("# engine forward passes of the scheduler workload, by row count, made by:")
+    print(f"#   rocprofv3 --kernel-trace --stats -f csv -d {trace_dir} -o bench -- "
+          "python3 bench.py --no-cpu")
+    print(f"#   python3 bench.py --summarize-sched {trace_dir}")
     for n in sorted(passes):
         ps = passes[n]
         if len(ps) < min_passes:
