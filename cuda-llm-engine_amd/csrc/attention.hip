@@ -19,11 +19,11 @@
 // (position, kv head): their q.k partial dots meet in three DPP steps, and every lane then owns
 // the scores of the 4 query heads that share its kv head.
 //
-// Each block (4 waves) takes a run of pages of one sequence (sequence-split grid) or of the
-// batch's pages laid end to end (page-balanced grid) for one kv group. Waves take chunks of
-// kChunk row reads in turn and keep an online softmax per query head (running max m and sum l
-// in log2 units, fp32 accumulators for their 8 dims), rescaling once per chunk. The block
-// merges its waves through LDS. A sequence in one piece gets its output written directly;
+// Each block (4 waves; 2 for the smallest batches in kv groups of 2) takes a run of pages of one
+// sequence (sequence-split grid) or of the batch's pages laid end to end (page-balanced grid)
+// for one kv group. Waves take chunks of kChunk row reads in turn and keep an online softmax
+// per query head (running max m and sum l in log2 units, fp32 accumulators for their 8 dims),
+// rescaling once per chunk. The block merges its waves through LDS. A sequence in one piece gets its output written directly;
 // otherwise each piece leaves an unnormalised partial (A, m, l) in the workspace and a second
 // kernel merges them.
 #include <math.h>
@@ -259,11 +259,14 @@ __device__ __forceinline__ void attend_partial_chunk(SoftmaxState& st,
   fold_chunk<KVW, false>(st, qv, c, ok);
 }
 
-// Per-block LDS: the waves' softmax states for the merge at the end of a segment.
-template <int KVW>
+// Per-block LDS: the softmax states of a block's W waves for the merge at the end of a segment.
+template <int KVW, int W = kWaves>
 struct MergeLds {
-  static constexpr int NP = kWaves * (8 / KVW);  // partial states per query head
-  static constexpr int HEADS = KVW * kGroup;     // query heads a block serves (32 for KVW = 8)
+  static constexpr int NP = W * (8 / KVW);    // partial states per query head
+  static constexpr int HEADS = KVW * kGroup;  // query heads a block serves (32 for KVW = 8)
+  // After the merge thread t holds query head t / 8: the block needs a thread for every dim
+  // octet of every head it serves.
+  static_assert(HEADS * 8 <= 64 * W, "too few threads for the kv group");
   float acc[NP][HEADS][kHeadDim];
   float m[NP][HEADS], l[NP][HEADS];
 };
@@ -292,22 +295,22 @@ __device__ __forceinline__ void load_query(u32x4 (&qv)[kGroup], const f16* __res
 
 // The block's attention over positions [pos0, pos1) of one sequence (all cached, in the pool
 // pages that `pages` names) for the query heads of kv group `kvg`, with the lane's query dims in
-// qv (load_query). On return thread t with t / 8 < HEADS holds the block's combined
-// unnormalised state of query head kvg * HEADS + t / 8, dims 8 * (t % 8) .. + 8: A (sum of
-// p * v), M (max score, log2 units) and L (sum of p). Ends with a barrier, so the LDS can be
-// reused at once.
+// qv (load_query), by a block of W waves. On return thread t with t / 8 < HEADS holds the
+// block's combined unnormalised state of query head kvg * HEADS + t / 8, dims 8 * (t % 8) ..
+// + 8: A (sum of p * v), M (max score, log2 units) and L (sum of p). Ends with a barrier, so
+// the LDS can be reused at once.
 // NJ > 0: the wave has at most NJ chunks whose every position is cached; their loads are all
 // issued before the first fold (one round trip for a short segment). NJ = 0: any number, streamed
 // two at a time.
-template <int KVW, int NJ = 0, class Pages>
+template <int KVW, int NJ = 0, int W = kWaves, class Pages>
 __device__ __forceinline__ void attend_segment(const u32x4 (&qv)[kGroup],
                                                const f16* __restrict__ k_pool,
                                                const f16* __restrict__ v_pool,
                                                const Pages& pages, int pos0, int pos1, int kvg,
-                                               int n_kv_heads, MergeLds<KVW>& lds,
+                                               int n_kv_heads, MergeLds<KVW, W>& lds,
                                                float (&A)[8], float& M, float& L) {
   constexpr int PPL = 8 / KVW;
-  constexpr int NP = MergeLds<KVW>::NP, HEADS = MergeLds<KVW>::HEADS;
+  constexpr int NP = MergeLds<KVW, W>::NP, HEADS = MergeLds<KVW, W>::HEADS;
   constexpr int ROWS = chunk_rows<KVW>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -337,7 +340,7 @@ __device__ __forceinline__ void attend_segment(const u32x4 (&qv)[kGroup],
   // They are double-buffered: the loads of chunk j + 1 are issued before chunk j is folded. The
   // steady loop issues its loads unconditionally; a conditional load would make the compiler
   // wait for every outstanding load, the new ones included, before each fold.
-  constexpr int STEP = kWaves * ROWS;
+  constexpr int STEP = W * ROWS;
   const int first = wave * ROWS;
   const int nj = first + ROWS <= full_rows ? (full_rows - first - ROWS) / STEP + 1 : 0;
   bool all[ROWS];  // unused by the FULL fold
@@ -447,15 +450,15 @@ __device__ __forceinline__ void store_nan(f16* __restrict__ out, int seq, int h,
 // block-table entries all at once, so that its first K/V loads follow one round trip.
 // The arguments are ordered so that those the block needs before its first K/V loads fill the
 // 16 kernel-argument dwords preloaded into scalar registers; the output pointers, needed last,
-// are read from the argument buffer.
-template <int KVW, int NJ, bool RUN>
-__global__ void __launch_bounds__(kThreads)
+// are read from the argument buffer. W: waves per block.
+template <int KVW, int NJ, bool RUN, int W>
+__global__ void __launch_bounds__(64 * W)
 k_attn_split(const int* __restrict__ block_tables, const int* __restrict__ seq_lens,
              int max_pages, int pages_per_split, int n_heads, int n_kv_heads, int num_splits,
              const f16* __restrict__ q, const f16* __restrict__ k_pool,
              const f16* __restrict__ v_pool, f16* __restrict__ out, float* __restrict__ part_o,
              float2* __restrict__ part_ml) {
-  __shared__ MergeLds<KVW> lds;
+  __shared__ MergeLds<KVW, W> lds;
   const int split = blockIdx.x, kvg = blockIdx.y, seq = blockIdx.z;
   const int* __restrict__ row = block_tables + (size_t)seq * max_pages;
   const int page0 = split * pages_per_split;
@@ -464,8 +467,8 @@ k_attn_split(const int* __restrict__ block_tables, const int* __restrict__ seq_l
   int S = seq_lens[seq];
   if constexpr (RUN) run.settle(S);
   const int P = seq_pages(S, max_pages);
-  const int h = kvg * MergeLds<KVW>::HEADS + (threadIdx.x >> 3);
-  const bool writer = (int)(threadIdx.x >> 3) < MergeLds<KVW>::HEADS && h < n_heads;
+  const int h = kvg * MergeLds<KVW, W>::HEADS + (threadIdx.x >> 3);
+  const bool writer = (int)(threadIdx.x >> 3) < MergeLds<KVW, W>::HEADS && h < n_heads;
   const int page1 = page0 + pages_per_split < P ? page0 + pages_per_split : P;
   const int pos1 = S < page1 * kPage ? S : page1 * kPage;
   float A[8], M, L;
@@ -477,16 +480,16 @@ k_attn_split(const int* __restrict__ block_tables, const int* __restrict__ seq_l
       if (split == 0 && writer) store_nan(out, seq, h, n_heads);
       return;
     }
-    attend_segment<KVW, NJ>(qv, k_pool, v_pool, run, page0 * kPage, pos1, kvg, n_kv_heads, lds,
-                            A, M, L);
+    attend_segment<KVW, NJ, W>(qv, k_pool, v_pool, run, page0 * kPage, pos1, kvg, n_kv_heads,
+                               lds, A, M, L);
   } else {
     if (page0 >= P) {
       if (split == 0 && writer) store_nan(out, seq, h, n_heads);
       return;
     }
     load_query<KVW>(qv, q, seq, kvg, n_heads);
-    attend_segment<KVW, NJ>(qv, k_pool, v_pool, TablePages{row}, page0 * kPage, pos1, kvg,
-                            n_kv_heads, lds, A, M, L);
+    attend_segment<KVW, NJ, W>(qv, k_pool, v_pool, TablePages{row}, page0 * kPage, pos1, kvg,
+                               n_kv_heads, lds, A, M, L);
   }
   if (!writer) return;
   if ((P + pages_per_split - 1) / pages_per_split == 1)
@@ -902,21 +905,38 @@ constexpr int kShortRunPages = kRunPages;
 // attend_segment's NJ for runs of pps pages: all of a wave's chunks in flight at once when it
 // has at most two, else 0 (streamed two at a time: with all four in flight, 188 VGPRs, 16 x 2048
 // measured 18.1 -> 19.1 us and 1 x 2048 10.4 -> 11.1 us).
-template <int KVW>
+template <int KVW, int W = kWaves>
 int short_run_chunks(int pps) {
   constexpr int PPL = 8 / KVW, ROWS = chunk_rows<KVW>();
   const int rows = pps * kPage / PPL;
-  const int per_wave = ((rows + ROWS - 1) / ROWS + kWaves - 1) / kWaves;
+  const int per_wave = ((rows + ROWS - 1) / ROWS + W - 1) / W;
   return per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : 0;
 }
 
-template <int KVW, int NJ, bool RUN>
+template <int KVW, int NJ, bool RUN, int W = kWaves>
 int split_launch(const AttnArgs& a, int groups, int pps, hipStream_t s) {
   const dim3 grid((unsigned)a.num_splits, (unsigned)groups, (unsigned)a.n_seq);
-  return launch(k_attn_split<KVW, NJ, RUN>, grid, dim3(kThreads), 0, s, a.tables, a.lens,
+  return launch(k_attn_split<KVW, NJ, RUN, W>, grid, dim3(64 * W), 0, s, a.tables, a.lens,
                 a.max_pages, pps, a.n_heads, a.n_kv_heads, a.num_splits, a.q, a.k_pool, a.v_pool,
                 a.out, a.part_o, a.part_ml);
 }
+
+// The short-run grid with W waves per block.
+template <int KVW, int W>
+int short_run_launch(const AttnArgs& a, int groups, int pps, hipStream_t s) {
+  switch (short_run_chunks<KVW, W>(pps)) {
+    case 1: return split_launch<KVW, 1, true, W>(a, groups, pps, s);
+    case 2: return split_launch<KVW, 2, true, W>(a, groups, pps, s);
+    default: return split_launch<KVW, 0, true, W>(a, groups, pps, s);
+  }
+}
+
+// Batches of at most this many (sequence, kv group) pairs in kv groups of 2 heads (one or two
+// sequences of 8 kv heads) run the short-run grid in 2-wave blocks: the block's chunks in half
+// as many waves, and half as many wave states to merge through LDS. Same box, 8 kv heads, 2048
+// positions, 32 splits: 1 sequence 8.12 -> 7.71 us, 2 sequences 8.50 -> 7.99. At 4 sequences
+// (groups of 4) 2-wave blocks were no faster (9.54 -> 9.63), and slower from 8 on.
+constexpr int kTwoWavePairs = 8;
 
 template <int KVW>
 int attn_launch(const AttnArgs& a, hipStream_t s) {
@@ -937,10 +957,12 @@ int attn_launch(const AttnArgs& a, hipStream_t s) {
   }
   int st;
   if (short_runs) {
-    switch (short_run_chunks<KVW>(pps)) {
-      case 1: st = split_launch<KVW, 1, true>(a, groups, pps, s); break;
-      case 2: st = split_launch<KVW, 2, true>(a, groups, pps, s); break;
-      default: st = split_launch<KVW, 0, true>(a, groups, pps, s); break;
+    if constexpr (KVW == 2) {
+      st = (long long)a.n_seq * groups <= kTwoWavePairs
+               ? short_run_launch<KVW, 2>(a, groups, pps, s)
+               : short_run_launch<KVW, kWaves>(a, groups, pps, s);
+    } else {
+      st = short_run_launch<KVW, kWaves>(a, groups, pps, s);
     }
   } else {
     st = split_launch<KVW, 0, false>(a, groups, pps, s);
