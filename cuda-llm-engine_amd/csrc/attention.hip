@@ -934,8 +934,9 @@ int short_run_launch(const AttnArgs& a, int groups, int pps, hipStream_t s) {
 // Batches of at most this many (sequence, kv group) pairs in kv groups of 2 heads (one or two
 // sequences of 8 kv heads) run the short-run grid in 2-wave blocks: the block's chunks in half
 // as many waves, and half as many wave states to merge through LDS. Same box, 8 kv heads, 2048
-// positions, 32 splits: 1 sequence 8.12 -> 7.71 us, 2 sequences 8.50 -> 7.99. At 4 sequences
-// (groups of 4) 2-wave blocks were no faster (9.54 -> 9.63), and slower from 8 on.
+// positions, 32 splits: 1 sequence 8.14 -> 7.72 us, 2 sequences 8.50 -> 7.99. At 4 sequences
+// (groups of 4) 2-wave blocks were no faster (9.54 -> 9.63), and slower from 8 on; 1-wave
+// blocks lose (8.84 us at 1 sequence).
 constexpr int kTwoWavePairs = 8;
 
 template <int KVW>
