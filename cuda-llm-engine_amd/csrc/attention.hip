@@ -23,9 +23,9 @@
 // sequence (sequence-split grid) or of the batch's pages laid end to end (page-balanced grid)
 // for one kv group. Waves take chunks of kChunk row reads in turn and keep an online softmax
 // per query head (running max m and sum l in log2 units, fp32 accumulators for their 8 dims),
-// rescaling once per chunk. The block merges its waves through LDS. A sequence in one piece gets its output written directly;
-// otherwise each piece leaves an unnormalised partial (A, m, l) in the workspace and a second
-// kernel merges them.
+// rescaling once per chunk. The block merges its waves through LDS. A sequence in one piece
+// gets its output written directly; otherwise each piece leaves an unnormalised partial
+// (A, m, l) in the workspace and a second kernel merges them.
 #include <math.h>
 
 #include <mutex>
