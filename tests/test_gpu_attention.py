@@ -167,6 +167,27 @@ def test_empty_sequences_give_nan_and_leave_the_rest_intact(llmk, orc):
                    "non-empty rows")
 
 
+@pytest.mark.parametrize("lens", [(0, 2048), (2048, -3), (0,), (1,), (1, 1), (1, 2048)])
+def test_smallest_batches_empty_and_single_positions(llmk, orc, lens):
+    """One or two sequences of 8 kv heads take 2-head kv groups, and at 3 or more splits of
+    short runs 2-wave blocks: an empty sequence gives NaN, a single cached position returns its
+    V row exactly, and the rest agrees with the oracle, at every split count."""
+    n = len(lens)
+    c = attention_case(np.random.default_rng(900 + 7 * n + sum(lens)), lens)
+    d = OnDevice(c)
+    ref = oracle_out(orc, c).reshape(n, -1)
+    for splits in (1, 3, 32):
+        got = d.run(llmk, splits, fill=0x1234).reshape(n, -1)
+        for b, L in enumerate(lens):
+            what = f"lens {lens} seq {b} splits {splits}"
+            if L <= 0:
+                assert np.all(np.isnan(got[b].view(np.float16))), what
+            elif L == 1:
+                assert np.array_equal(got[b], ref[b]), what
+            else:
+                assert_tol(orc.compare(got[b], ref[b]), EXACT_FLOOR, what)
+
+
 def test_single_position_returns_the_value_row_exactly(llmk, orc):
     """Weight exactly 1: out = the V row, bit for bit, whatever the split count."""
     c = attention_case(np.random.default_rng(6), (1,) * 9)
