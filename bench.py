@@ -58,7 +58,7 @@ SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_819
             "pass_floor_stages", "attention_256", "attention_16x2048", "attention_sweep",
             "argmax", "step_256", "step_8", "sched", "probe_sweep", "probe_kernels", "copy_1GiB",
             "residual_add", "rmsnorm_8192", "kv_scatter_8192", "kv_scatter_batch_256",
-            "pass2_graph", "pass2_layers", "end", "setup"]
+            "pass2_graph", "pass2_layers", "pass_fused", "pass2_fused", "end", "setup"]
 
 # Launch shapes (blocks, threads) of the 16-layer pass at 256 sequences, from the launchers'
 # grid rules: the embedding and add+RMSNorm take one 64-thread wave per row below 4096 rows
@@ -165,6 +165,11 @@ PROFILE_SHAPES = [
     # the pass with one launch per layer: 256 norm rows, 256 RoPE tokens, 4096 SwiGLU chunks
     ("decode_layers:layer_256", "pass_layers", "k_layer_passILi4ELb0ELi6ELb0E|k_layer_pass<4, false, 6, false>",
      4608 * 64, 4198400 + 3147904 + 12582912),
+    # the whole pass in one launch: 256 residual chains, 16 x 256 RoPE tokens, 16 x 4096 SwiGLU
+    # chunks; bytes: what it must move (config 5's count less the residual rows it keeps in
+    # registers, workloads.bytes_decode_pass_fused)
+    ("decode_fused:pass_256", "pass_fused", "k_layers_fusedILi4ELi6ELb0ELb1E|k_layers_fused<4, 6, false, true>",
+     (256 + 16 * 256 + 16 * 4096) * 64, 303139840),
 ]
 
 
@@ -298,6 +303,10 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
     summarize_pass(tagged, "pass2_graph", "k_embedding", 65)
     print("#")
     summarize_pass(tagged, "pass2_layers", "k_layer_passILi4ELb1E|k_layer_pass<4, true", 16)
+    print("#")
+    summarize_pass(tagged, "pass_fused", "k_layers_fused", 1)
+    print("#")
+    summarize_pass(tagged, "pass2_fused", "k_layers_fused", 1)
     return 1 if missing else 0
 
 
@@ -808,7 +817,16 @@ class Bench:
         self.kernels["decode_pass_16x256_two_norms_layers"] = kernel_entry(
             "decode pass, both norms, one launch per layer", nb, t, None,
             {"launches": L, "layers": L, "seqs": n, "sets": 2})
-        del lgraphs, dps, ps
+        del lgraphs
+        fgraphs = [capture(dp.run_fused) for dp in dps]
+        self.mark("pass2_fused")
+        t = self.run(lambda i: fgraphs[i].replay(), 2, steps, warm)
+        moved = wl.bytes_decode_pass_fused(n, L, two_norms=True)
+        self.kernels["decode_pass_16x256_two_norms_fused"] = kernel_entry(
+            "decode pass, both norms, one launch", nb, t, None,
+            {"launches": 1, "layers": L, "seqs": n, "sets": 2, "moved_bytes": moved,
+             "moved_frac_of_peak": round(moved / t["mean_s"] / 1e9 / PEAK_GBS, 4)})
+        del fgraphs, dps, ps
         self.free()
 
     # ------------------------------------------------------------------ config 5
@@ -874,6 +892,22 @@ class Bench:
                      "per-layer inputs are independent, not for a decode step with GEMMs "
                      "between the ops"})
         del lgraphs
+        # the whole pass in one launch (llmk_decode_nongemm_pass_fused): the residual chains of
+        # all 16 layers beside every layer's RoPE + scatter tokens and SwiGLU chunks
+        fgraphs = [capture(dp.run_fused) for dp in dps]
+        self.mark("pass_fused")
+        t = self.run(lambda i: fgraphs[i].replay(), 2, steps, warm)
+        moved = wl.bytes_decode_pass_fused(n, L)
+        self.kernels["decode_pass_16x256_fused"] = kernel_entry(
+            "decode pass, one launch (graph)", nb, t, None,
+            {"launches": 1, "layers": L, "seqs": n, "sets": 2, "moved_bytes": moved,
+             "moved_frac_of_peak": round(moved / t["mean_s"] / 1e9 / PEAK_GBS, 4),
+             "note": "one wave per sequence carries the residual through all 16 layers' add + "
+                     "RMSNorm (stored after every layer, never re-read) while the other blocks "
+                     "run every layer's RoPE + K/V scatter and SwiGLU; `bytes` is config 5's "
+                     "count, `moved_bytes` what this launch must move (no embedding rows "
+                     "written and re-read, no residual re-read per layer)"})
+        del fgraphs
 
         # ---- breakdown
         def stage_fn(op, p):

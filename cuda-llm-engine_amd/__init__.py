@@ -155,6 +155,7 @@ _SIGS = {
     "llmk_attention_decode_fast_noalloc": (_i, [_vp] * 6 + [_i] * 7 + [_vp]),
     "llmk_decode_nongemm_pass": (_i, [ctypes.POINTER(DecodePass), _vp]),
     "llmk_decode_nongemm_pass_layers": (_i, [ctypes.POINTER(DecodePass), _vp]),
+    "llmk_decode_nongemm_pass_fused": (_i, [ctypes.POINTER(DecodePass), _vp]),
     "llmk_blas_create": (_i, [ctypes.POINTER(_vp)]),
     "llmk_blas_destroy": (None, [_vp]),
     "llmk_linear": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
@@ -569,6 +570,11 @@ class DecodeNonGemmPass:
         """The same pass with one launch per layer (``llmk_decode_nongemm_pass_layers``)."""
         _check("decode_nongemm_pass_layers",
                _lib.llmk_decode_nongemm_pass_layers(ctypes.byref(self._desc), _stream(stream)))
+
+    def run_fused(self, stream=None) -> None:
+        """The same pass in one launch per 16 layers (``llmk_decode_nongemm_pass_fused``)."""
+        _check("decode_nongemm_pass_fused",
+               _lib.llmk_decode_nongemm_pass_fused(ctypes.byref(self._desc), _stream(stream)))
 
 
 # ---------------------------------------------------------------------------------------------

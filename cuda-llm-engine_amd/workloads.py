@@ -95,6 +95,15 @@ def bytes_decode_pass(n: int, layers: int, two_norms: bool = False) -> int:
     return bytes_embedding(n, HIDDEN) + layers * per_layer
 
 
+def bytes_decode_pass_fused(n: int, layers: int, two_norms: bool = False) -> int:
+    """What the fused pass (llmk_decode_nongemm_pass_fused) must move: config 5's bytes less
+    the residual rows it keeps in registers -- the embedding rows are not written and re-read,
+    and per layer the residual is stored once (after its last add) and never re-read."""
+    row = n * HIDDEN * 2
+    saved = row + layers * (3 if two_norms else 1) * row
+    return bytes_decode_pass(n, layers, two_norms) - saved
+
+
 def bytes_attention(lens: np.ndarray, nh: int = N_HEADS, nkv: int = N_KV,
                     hd: int = HEAD_DIM) -> int:
     """Cached K and V rows of every sequence read once, q read and out written once, plus the

@@ -270,6 +270,16 @@ LLMK_API int llmk_decode_nongemm_pass(const llmk_decode_pass* pass, void* stream
  * llmk_decode_nongemm_pass). */
 LLMK_API int llmk_decode_nongemm_pass_layers(const llmk_decode_pass* pass, void* stream);
 
+/* The same pass and results in one launch per 16 layers (config 5's pass is one launch): one
+ * wave per sequence carries its residual row through all of the launch's layers (each layer's
+ * add + RMSNorm, or both of them, in order, the residual kept in registers and stored after
+ * every layer), while the other blocks of the launch run every layer's RoPE + K/V scatter
+ * tokens and SwiGLU chunks. Valid for the same reason and under the same requirements as
+ * llmk_decode_nongemm_pass_layers, and hidden <= 4096 (LLMK_ERR_UNSUPPORTED above: use
+ * llmk_decode_nongemm_pass_layers). New entry point; the reference runs these ops as separate
+ * launches (engine/batched.cu:44-72,112-116). */
+LLMK_API int llmk_decode_nongemm_pass_fused(const llmk_decode_pass* pass, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * The decode step around the kernels above: projections (hipBLASLt), the fused layouts they
  * produce, and an engine that runs a whole Llama-3 forward pass over a batch of token rows.

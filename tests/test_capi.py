@@ -164,7 +164,8 @@ def test_decode_pass_descriptor_validation_without_launch(llmk):
             setattr(d, f, v)
         return ctypes.byref(d)
 
-    for fn in (L.llmk_decode_nongemm_pass, L.llmk_decode_nongemm_pass_layers):
+    for fn in (L.llmk_decode_nongemm_pass, L.llmk_decode_nongemm_pass_layers,
+               L.llmk_decode_nongemm_pass_fused):
         assert fn(desc(x2=parr), None) == E.LLMK_ERR_INVALID_VALUE
         assert fn(desc(x2=parr, norm_w2=parr), None) == E.LLMK_ERR_INVALID_VALUE
         assert fn(desc(normed2=parr), None) == E.LLMK_ERR_INVALID_VALUE

@@ -234,9 +234,10 @@ def _pass_pair(llmk, wl, inv, **kw):
     return out
 
 
-def _same_pass_bits(pa, da, pb, db):
-    """Runs the op-by-op pass on set a and the one-launch-per-layer pass on set b (whose
-    outputs start as NaN) and compares every output bit for bit."""
+def _same_pass_bits(pa, da, pb, db, method="run_layers"):
+    """Runs the op-by-op pass on set a and, on set b (whose outputs start as NaN), the pass
+    ``method`` names (one launch per layer, or the fused one), and compares every output bit for
+    bit."""
     for L in pa.per_layer:
         L["act"].zero_()
         L["normed"].zero_()
@@ -247,7 +248,7 @@ def _same_pass_bits(pa, da, pb, db):
             L["normed2"].fill_(float("nan"))
     pb.residual.fill_(float("nan"))
     da.run()
-    db.run_layers()
+    getattr(db, method)()
     torch.cuda.synchronize()
     assert torch.equal(pa.residual.view(torch.int16), pb.residual.view(torch.int16))
     for l, (A, B) in enumerate(zip(pa.per_layer, pb.per_layer)):
@@ -308,6 +309,64 @@ def test_decode_pass_one_launch_per_layer_refuses_other_shapes(llmk, wl, inv):
         dp.run_layers()
     assert err.value.status == llmk.LLMK_ERR_UNSUPPORTED
     dp.run()
+    torch.cuda.synchronize()
+    assert torch.isfinite(p.residual).all()
+
+
+@pytest.mark.parametrize("shape", [dict(n=64, layers=3, max_pages=32, seed=0x5EED0000 + 60),
+                                   dict(n=37, layers=1, max_pages=8, seed=0x5EED0000 + 61),
+                                   dict(n=29, layers=19, max_pages=8, seed=0x5EED0000 + 62),
+                                   dict()],
+                         ids=["64x3", "37x1", "29x19_two_launches", "config5"])
+def test_decode_pass_fused_gives_the_bits_of_the_op_by_op_pass(llmk, wl, inv, shape):
+    """llmk_decode_nongemm_pass_fused (one launch per 16 layers: each sequence's residual chain
+    through every layer by one wave, beside every layer's RoPE + scatter tokens and SwiGLU
+    chunks) against llmk_decode_nongemm_pass: residual, normed rows, rotated Q, SwiGLU output
+    and whole K and V pools of every layer, bit for bit. Shapes: a small pass, one layer of 37
+    sequences (partial last SwiGLU chunk), 19 layers (a launch of 16 and one of 3, the second
+    starting from the residual the first left), and config 5 (256 x 16: one launch)."""
+    (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **shape)
+    _same_pass_bits(pa, da, pb, db, "run_fused")
+
+
+@pytest.mark.parametrize("model,two_norms",
+                         [(m, False) for m in PASS_MODELS if m[0] <= 4096]
+                         + [(PASS_MODELS[0], True), (PASS_MODELS[1], True),
+                            (PASS_MODELS[2], True), (PASS_MODELS[3], True)],
+                         ids=lambda v: ("h%d_q%d_kv%d" % v[:3]) if isinstance(v, tuple)
+                         else ("two_norms" if v else "one_norm"))
+def test_decode_pass_fused_across_model_shapes(llmk, wl, inv, model, two_norms):
+    """The fused pass against the op-by-op pass at every row width it takes (hidden 512-4096:
+    1, 2, 4, 8 vectors per lane, each with its own prefetch depth) and every RoPE task count,
+    with one and with both of a layer's norms: 29 sequences, 3 layers, bit for bit."""
+    hidden, nh, nkv, inter = model
+    kw = dict(n=29, layers=3, max_pages=8, seed=0x5EED0000 + 63, hidden=hidden, n_heads=nh,
+              n_kv=nkv, inter=inter, vocab=1000, two_norms=two_norms)
+    (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, **kw)
+    _same_pass_bits(pa, da, pb, db, "run_fused")
+
+
+def test_decode_pass_fused_two_norms_config5(llmk, wl, inv):
+    """The fused pass with both of the real layer's add + RMSNorm pairs, at config 5's shape
+    (256 sequences, 16 layers, one launch), against the op-by-op pass, bit for bit."""
+    (pa, da), (pb, db) = _pass_pair(llmk, wl, inv, two_norms=True)
+    _same_pass_bits(pa, da, pb, db, "run_fused")
+
+
+def test_decode_pass_fused_refuses_wide_rows(llmk, wl, inv):
+    """Rows wider than 4096 (hidden 8192) are refused by the fused pass with
+    LLMK_ERR_UNSUPPORTED; the one-launch-per-layer pass takes them."""
+    hidden, nh, nkv, inter = PASS_MODELS[4]
+    p = wl.decode_pass_inputs(inv[1], n=5, layers=1, max_pages=4, seed=0x5EED0000 + 64,
+                              hidden=hidden, n_heads=nh, n_kv=nkv, inter=inter, vocab=100)
+    dp = llmk.DecodeNonGemmPass(p.table, p.token_ids, p.residual, p.block_tables, p.positions,
+                                p.inv_freq, p.per_layer, n_heads=nh, n_kv_heads=nkv,
+                                head_dim=wl.HEAD_DIM, inter=inter, page_size=wl.PAGE,
+                                max_pages=p.max_pages, eps=EPS)
+    with pytest.raises(llmk.LlmkError) as err:
+        dp.run_fused()
+    assert err.value.status == llmk.LLMK_ERR_UNSUPPORTED
+    dp.run_layers()
     torch.cuda.synchronize()
     assert torch.isfinite(p.residual).all()
 
