@@ -679,8 +679,7 @@ class Bench:
             "ids": [s["ids"].cpu().numpy().copy() for s in sets5]}
         self.mark("embedding_8192")
         t = self.run(lambda i: llmk.embedding_lookup(sets5[i]["table"], sets5[i]["ids"],
-                                                     sets5[i]["out"], 8192, hidden,
-                                                     check_indices=False), R5)
+                                                     sets5[i]["out"], 8192, hidden), R5)
         self.kernels["embedding_8192"] = kernel_entry(
             "embedding_lookup 8192 of 128256", wl.bytes_embedding(8192, hidden), t,
             self.traffic.get("embedding_8192"),
@@ -737,7 +736,7 @@ class Bench:
             "table": sc[0]["table"].cpu().numpy().copy(), "pages": pages}
         self.mark("kv_scatter_8192")
         t = self.run(lambda i: llmk.kv_scatter(sc[i]["src"], sc[i]["pool"], sc[i]["table"], 0, T,
-                                               ps, kvdim, check_indices=False), R)
+                                               ps, kvdim), R)
         self.kernels["kv_scatter_8192"] = kernel_entry(
             "kv_scatter 8192 rows (prefill)", nb, t, self.traffic.get("kv_scatter_8192"),
             {"sets": R, "pages": pages})
@@ -764,7 +763,7 @@ class Bench:
             "pos": (lens - 1).astype(np.int32), "total": total}
         self.mark("kv_scatter_batch_256")
         t = self.run(lambda i: llmk.kv_scatter_batch(srcs[i], pool, dtab, dpos, n, max_pages, ps,
-                                                     kvdim, check_indices=False), R)
+                                                     kvdim), R)
         self.kernels["kv_scatter_batch_256"] = kernel_entry(
             "kv_scatter_batch 256 sequences", wl.bytes_kv_scatter_batch(n, kvdim), t,
             self.traffic.get("kv_scatter_batch_256"),
@@ -913,8 +912,7 @@ class Bench:
         def stage_fn(op, p):
             def f():
                 if op == "embedding":
-                    llmk.embedding_lookup(p.table, p.token_ids, p.residual, n, wl.HIDDEN,
-                                          check_indices=False)
+                    llmk.embedding_lookup(p.table, p.token_ids, p.residual, n, wl.HIDDEN)
                 for lay in (p.per_layer if op != "embedding" else ()):
                     if op == "add_rmsnorm":
                         llmk.add_rmsnorm(p.residual, lay["x"], lay["norm_w"], lay["normed"], n,
@@ -923,8 +921,7 @@ class Bench:
                         llmk.rope_kv_scatter_batch(lay["q"], lay["k"], lay["v"], lay["k_pool"],
                                                    lay["v_pool"], p.block_tables, p.positions,
                                                    p.inv_freq, n, p.max_pages, wl.PAGE,
-                                                   wl.N_HEADS, wl.N_KV, wl.HEAD_DIM,
-                                                   check_indices=False)
+                                                   wl.N_HEADS, wl.N_KV, wl.HEAD_DIM)
                     elif op == "swiglu":
                         llmk.swiglu(lay["gate"], lay["up"], lay["act"], n * wl.INTER)
             return f
@@ -997,7 +994,7 @@ class Bench:
                 llmk.attention_decode_fast(a["q"], a["k_pool"], a["v_pool"], a["block_tables"],
                                            a["seq_lens"], a["out"], a["workspace"], a["n"],
                                            a["max_pages"], wl.PAGE, wl.N_HEADS, wl.N_KV,
-                                           wl.HEAD_DIM, splits, check_indices=False)
+                                           wl.HEAD_DIM, splits)
 
             self.mark(section)
             t = self.run(launch_attn, R)

@@ -7,9 +7,12 @@ all compute is libllmk's HIP kernels). ``stream=None`` means torch's current str
 
 Errors: a violated precondition raises ``LlmkError`` before anything is launched. Besides the
 C-ABI's own checks, every function verifies here that each tensor holds at least the elements
-the kernel will touch, and (``check_indices=True``, the default, at the cost of a device sync)
-that token ids, page numbers and positions address only rows that exist, so that a kernel is
-never launched on operands that do not fit it.
+the kernel will touch. Checking the values inside the index tensors -- that token ids, page
+numbers and positions address only rows that exist -- reads them back, a device
+synchronisation per call, so it is off by default, as in the reference, whose launchers check
+nothing (kernels/embedding.cuh:5). Turn it on per call (``check_indices=True``), for every call
+(``set_check_indices(True)``, or ``LLMK_CHECK_INDICES=1`` in the environment), or build a
+``DecodeNonGemmPass``, which validates its indices once, when it is built.
 
 There is no CPU fallback: if libllmk.so is missing, importing this package raises.
 """
@@ -22,6 +25,18 @@ import re
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
+_CHECK_INDICES = os.environ.get("LLMK_CHECK_INDICES", "") not in ("", "0")
+
+
+def set_check_indices(on: bool) -> None:
+    """Default of every function's ``check_indices`` argument (initially off, or on with
+    ``LLMK_CHECK_INDICES=1``): validate the index tensors' values on the host before launching."""
+    global _CHECK_INDICES
+    _CHECK_INDICES = bool(on)
+
+
+def _want_checks(flag) -> bool:
+    return _CHECK_INDICES if flag is None else bool(flag)
 LIB_PATH = os.path.join(_HERE, "libllmk.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "llmk.h")
 
@@ -261,7 +276,7 @@ def _range_check(fn: str, t: torch.Tensor, n: int, lo: int, hi: int, name: str) 
 # operators (ref: kernels/*.cuh)
 # ---------------------------------------------------------------------------------------------
 def embedding_lookup(table, ids, out, n_tokens: int, hidden: int, stream=None,
-                     check_indices: bool = True) -> None:
+                     check_indices: bool | None = None) -> None:
     """out[t] = table[ids[t]] (ref: kernels/embedding.cuh:6-7)."""
     fn = "embedding_lookup"
     if table.dim() != 2 or table.shape[1] != hidden:
@@ -269,7 +284,7 @@ def embedding_lookup(table, ids, out, n_tokens: int, hidden: int, stream=None,
     pt = _dev(fn, table, torch.float16, 0, "table")
     pi = _dev(fn, ids, torch.int32, n_tokens, "ids")
     po = _dev(fn, out, torch.float16, n_tokens * hidden, "out")
-    if check_indices:
+    if _want_checks(check_indices):
         _range_check(fn, ids, n_tokens, 0, table.shape[0], "ids")
     _check(fn, _lib.llmk_embedding_lookup(pt, pi, po, n_tokens, hidden, _stream(stream)))
 
@@ -342,7 +357,7 @@ def _pool_rows(fn: str, pool, kvdim: int) -> int:
 
 
 def kv_scatter(src, pool, block_table, start_pos: int, T: int, page_size: int, kvdim: int,
-               stream=None, check_indices: bool = True) -> None:
+               stream=None, check_indices: bool | None = None) -> None:
     """Prefill scatter of T rows into pages (ref: kernels/kv_scatter.cuh:7-8)."""
     fn = "kv_scatter"
     if T > 0 and (start_pos < 0 or page_size <= 0):
@@ -351,7 +366,7 @@ def kv_scatter(src, pool, block_table, start_pos: int, T: int, page_size: int, k
     ps = _dev(fn, src, torch.float16, T * kvdim, "src")
     pp = _dev(fn, pool, torch.float16, 0, "pool")
     pt = _dev(fn, block_table, torch.int32, n_table, "block_table")
-    if check_indices and T > 0:
+    if _want_checks(check_indices) and T > 0:
         rows = _pool_rows(fn, pool, kvdim)
         first = start_pos // page_size
         _range_check(fn, block_table[first:n_table], n_table - first, 0, rows // page_size,
@@ -369,14 +384,15 @@ def _check_batch_tables(fn, block_tables, positions, pools, n, max_pages, page_s
 
 
 def kv_scatter_batch(src, pool, block_tables, positions, n: int, max_pages: int,
-                     page_size: int, kvdim: int, stream=None, check_indices: bool = True) -> None:
+                     page_size: int, kvdim: int, stream=None,
+                     check_indices: bool | None = None) -> None:
     """Decode scatter, one row per sequence (ref: kernels/kv_scatter.cuh:12-13)."""
     fn = "kv_scatter_batch"
     ps = _dev(fn, src, torch.float16, n * kvdim, "src")
     pp = _dev(fn, pool, torch.float16, 0, "pool")
     pt = _dev(fn, block_tables, torch.int32, n * max_pages, "block_tables")
     pq = _dev(fn, positions, torch.int32, n, "positions")
-    if check_indices and n > 0:
+    if _want_checks(check_indices) and n > 0:
         _check_batch_tables(fn, block_tables, positions, [pool], n, max_pages, page_size, kvdim)
     _check(fn, _lib.llmk_kv_scatter_batch(ps, pp, pt, pq, n, max_pages, page_size, kvdim,
                                           _stream(stream)))
@@ -384,7 +400,7 @@ def kv_scatter_batch(src, pool, block_tables, positions, n: int, max_pages: int,
 
 def rope_kv_scatter_batch(q, k, v, k_pool, v_pool, block_tables, positions, inv_freq, n: int,
                           max_pages: int, page_size: int, n_heads: int, n_kv_heads: int,
-                          head_dim: int, stream=None, check_indices: bool = True) -> None:
+                          head_dim: int, stream=None, check_indices: bool | None = None) -> None:
     """Fused decode RoPE of q (in place) and k, with k and v scattered into their pools."""
     fn = "rope_kv_scatter_batch"
     kvdim = n_kv_heads * head_dim
@@ -396,7 +412,7 @@ def rope_kv_scatter_batch(q, k, v, k_pool, v_pool, block_tables, positions, inv_
     pt = _dev(fn, block_tables, torch.int32, n * max_pages, "block_tables")
     pp = _dev(fn, positions, torch.int32, n, "positions")
     pf = _dev(fn, inv_freq, torch.float32, head_dim // 2, "inv_freq")
-    if check_indices and n > 0:
+    if _want_checks(check_indices) and n > 0:
         _check_batch_tables(fn, block_tables, positions, [k_pool, v_pool], n, max_pages,
                             page_size, kvdim)
     _check(fn, _lib.llmk_rope_kv_scatter_batch(pq, pk, pv, pkp, pvp, pt, pp, pf, n, max_pages,
@@ -426,7 +442,7 @@ def attention_decode_fast_workspace_floats(n_seq: int, n_heads: int, num_splits:
 def attention_decode_fast(q, k_pool, v_pool, block_tables, seq_lens, out, workspace, n_seq: int,
                           max_pages: int, page_size: int, n_heads: int, n_kv_heads: int,
                           head_dim: int, num_splits: int, stream=None,
-                          check_indices: bool = True) -> None:
+                          check_indices: bool | None = None) -> None:
     """Split-KV decode attention over the paged pool (ref: kernels/attention_decode_fast.cuh:14-18).
 
     With ``check_indices`` the binding also checks, on the host, that every sequence length
@@ -444,7 +460,8 @@ def attention_decode_fast(q, k_pool, v_pool, block_tables, seq_lens, out, worksp
     pw = 0
     if workspace is not None:
         pw = _dev(fn, workspace, torch.float32, ws_need if num_splits > 1 else 0, "workspace")
-    if check_indices and n_seq > 0 and max_pages > 0 and page_size > 0 and kvdim > 0:
+    if (_want_checks(check_indices) and n_seq > 0 and max_pages > 0 and page_size > 0
+            and kvdim > 0):
         _range_check(fn, seq_lens, n_seq, -(1 << 31), max_pages * page_size + 1, "seq_lens")
         lens = seq_lens[:n_seq].long().clamp(min=0)
         npages = (lens + page_size - 1) // page_size
@@ -706,7 +723,7 @@ def blas_tune(handle: Blas, x, w, y, T: int, in_features: int, out_features: int
 
 def qkv_rope_scatter(qkv, ld: int, q_out, k_pool, v_pool, block_tables, positions, inv_freq,
                      n: int, max_pages: int, page_size: int, n_heads: int, n_kv_heads: int,
-                     head_dim: int, stream=None, check_indices: bool = True) -> None:
+                     head_dim: int, stream=None, check_indices: bool | None = None) -> None:
     """RoPE + KV scatter from the rows of a fused QKV projection (``llmk_qkv_rope_scatter``)."""
     fn = "qkv_rope_scatter"
     kvdim = n_kv_heads * head_dim
@@ -720,7 +737,7 @@ def qkv_rope_scatter(qkv, ld: int, q_out, k_pool, v_pool, block_tables, position
     pt = _dev(fn, block_tables, torch.int32, n * max_pages, "block_tables")
     pp = _dev(fn, positions, torch.int32, n, "positions")
     pi = _dev(fn, inv_freq, torch.float32, head_dim // 2, "inv_freq")
-    if check_indices and n > 0:
+    if _want_checks(check_indices) and n > 0:
         _check_batch_tables(fn, block_tables, positions, [k_pool, v_pool], n, max_pages,
                             page_size, kvdim)
     _check(fn, _lib.llmk_qkv_rope_scatter(pqkv, ld, pq, pk, pv, pt, pp, pi, n, max_pages,

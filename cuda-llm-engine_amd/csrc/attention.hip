@@ -987,7 +987,11 @@ using namespace llmk;
 extern "C" size_t llmk_attention_decode_fast_workspace_floats(int n_seq, int n_heads,
                                                              int num_splits) {
   if (n_seq <= 0 || n_heads <= 0 || num_splits <= 0) return 0;
-  return (size_t)n_seq * n_heads * num_splits * (kHeadDim + 2);
+  // Below 2^100 for any int arguments; SIZE_MAX when it does not fit a size_t, so that no
+  // product wraps to a size some buffer could hold.
+  const unsigned __int128 f =
+      (unsigned __int128)n_seq * (unsigned)n_heads * (unsigned)num_splits * (kHeadDim + 2);
+  return f > (unsigned __int128)SIZE_MAX ? SIZE_MAX : (size_t)f;
 }
 
 // Argument checks shared by both entry points; -1 means "go ahead".
@@ -1068,6 +1072,11 @@ extern "C" int llmk_attention_decode_fast(const uint16_t* q, const uint16_t* k_p
                                  num_splits);
   if (st != -1) return st;
   if (num_splits > 1 && !workspace) return LLMK_ERR_INVALID_VALUE;
+  // A workspace no allocation can hold (the size saturates): its slot offsets would not fit a
+  // size_t either.
+  if (num_splits > 1 &&
+      llmk_attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits) == SIZE_MAX)
+    return LLMK_ERR_INVALID_VALUE;
   if (workspace && !aligned16(workspace)) return LLMK_ERR_ALIGNMENT;
   return run_attention(q, k_pool, v_pool, block_tables, seq_lens, out, workspace, n_seq,
                        max_pages, n_heads, n_kv_heads, num_splits, stream);
@@ -1120,6 +1129,8 @@ extern "C" int llmk_attention_decode_fast_noalloc(const uint16_t* q, const uint1
                                  max_pages, page_size, n_heads, n_kv_heads, head_dim,
                                  num_splits);
   if (st != -1) return st;
+  // The size saturates rather than wraps (llmk_attention_decode_fast_workspace_floats), so a
+  // call whose partials would not fit is refused here whatever its arguments' magnitudes.
   const size_t need = llmk_attention_decode_fast_workspace_floats(n_seq, n_heads, num_splits);
   if (need > kScratchFloats) return LLMK_ERR_SCRATCH;
   float* ws = nullptr;

@@ -139,7 +139,9 @@ LLMK_API int llmk_rope_kv_scatter_batch(uint16_t* q, const uint16_t* k, const ui
 
 /* Floats of workspace llmk_attention_decode_fast needs for n_seq sequences, n_heads query
  * heads and up to num_splits splits per sequence: n_seq * n_heads * num_splits * (64 + 2), the
- * reference's figure. 0 for non-positive arguments.
+ * reference's figure. 0 for non-positive arguments; SIZE_MAX when the product exceeds the size_t
+ * range (it saturates instead of wrapping; llmk_attention_decode_fast then refuses the call with
+ * LLMK_ERR_INVALID_VALUE, the allocation-free variant with LLMK_ERR_SCRATCH).
  * ref: kernels/attention_decode_fast.cuh:6, kernels/attention_decode_fast.cu:151-153. */
 LLMK_API size_t llmk_attention_decode_fast_workspace_floats(int n_seq, int n_heads,
                                                             int num_splits);
@@ -290,6 +292,11 @@ LLMK_API int llmk_decode_nongemm_pass_fused(const llmk_decode_pass* pass, void* 
  * stream, or one handle per stream), as calls on one cuBLAS handle are. */
 typedef struct llmk_blas llmk_blas;
 LLMK_API int llmk_blas_create(llmk_blas** out);
+/* Lifetime: a HIP graph that captured llmk_linear (or llmk_blas_tune) on this handle holds its
+ * workspace address and hipBLASLt's kernels by reference. Destroy every such graph and graph
+ * exec, and let the work already launched from them finish, before destroying the handle.
+ * Destroying the handle first leaves those graphs pointing at freed memory and at kernels of
+ * code objects the handle has released. */
 LLMK_API void llmk_blas_destroy(llmk_blas* h);
 
 /* y[T, out_features] = x[T, in_features] * W^T, W stored [out_features, in_features] row-major
@@ -398,6 +405,11 @@ typedef struct llmk_layer_weights {
 typedef struct llmk_engine llmk_engine;
 LLMK_API int llmk_engine_create(const llmk_model_config* cfg, int max_rows, int max_pages,
                                 int num_pages, llmk_engine** out);
+/* Lifetime: the engine's own graphs (llmk_engine_forward_graph) are destroyed here, first. A
+ * graph the caller captured around llmk_engine_forward (or around anything reading the
+ * engine's buffers) references the engine's buffers, its GEMM handle's workspace and
+ * hipBLASLt's kernels: destroy it, and let its launched work finish, before destroying the
+ * engine. */
 LLMK_API void llmk_engine_destroy(llmk_engine* e);
 
 /* Copies the weights (host or device pointers; layers[n_layers]) into the engine. Synchronous. */

@@ -220,3 +220,35 @@ def test_no_oracle_in_the_product():
     out = subprocess.run(["ldd", os.path.join(pkg, "libllmk.so")], capture_output=True,
                          text=True, check=True).stdout
     assert "oracle" not in out
+
+
+def test_attention_workspace_size_saturates_instead_of_wrapping(llmk):
+    """llmk_attention_decode_fast_workspace_floats returns SIZE_MAX when the product does not fit
+    a size_t (it would wrap to 0 for 32768 sequences x 2^18 heads x 2^29 splits x 66); the
+    allocation-free entry point then refuses the call (LLMK_ERR_SCRATCH) and the workspace one
+    as well (LLMK_ERR_INVALID_VALUE), before anything is launched."""
+    lib = llmk.lib()
+    size_max = (1 << 64) - 1
+    assert lib.llmk_attention_decode_fast_workspace_floats(1 << 15, 1 << 18, 1 << 29) == size_max
+    assert lib.llmk_attention_decode_fast_workspace_floats(256, 32, 32) == 256 * 32 * 32 * 66
+    fake = 0x10000  # 16-byte aligned; never dereferenced: both calls return before any launch
+    args = [fake] * 6
+    n_seq, n_kv, splits = 1 << 15, 1 << 16, 1 << 29
+    assert lib.llmk_attention_decode_fast_noalloc(*args, n_seq, 128, 16, 4 * n_kv, n_kv, 64,
+                                                  splits, None) == llmk.LLMK_ERR_SCRATCH
+    assert lib.llmk_attention_decode_fast(*args, fake, n_seq, 128, 16, 4 * n_kv, n_kv, 64,
+                                          splits, None) == llmk.LLMK_ERR_INVALID_VALUE
+
+
+def test_index_checks_are_opt_in(llmk):
+    """The binding validates index values only when asked (per call, or module-wide), as the
+    reference's launchers check nothing; off by default unless LLMK_CHECK_INDICES is set."""
+    import os
+    env_on = os.environ.get("LLMK_CHECK_INDICES", "") not in ("", "0")
+    assert llmk._want_checks(None) == env_on
+    assert llmk._want_checks(True) and not llmk._want_checks(False)
+    llmk.set_check_indices(True)
+    try:
+        assert llmk._want_checks(None)
+    finally:
+        llmk.set_check_indices(env_on)

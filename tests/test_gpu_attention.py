@@ -235,7 +235,15 @@ def test_binding_rejects_lengths_beyond_the_table(llmk, reference_case):
     with pytest.raises(llmk.LlmkError):
         llmk.attention_decode_fast(d.q, d.kp, d.vp, d.tables, dev_i32(bad), out, None,
                                    reference_case["n_seq"], reference_case["max_pages"], 16, 32,
-                                   8, 64, 1)
+                                   8, 64, 1, check_indices=True)
+    llmk.set_check_indices(True)  # the same through the module-wide default
+    try:
+        with pytest.raises(llmk.LlmkError):
+            llmk.attention_decode_fast(d.q, d.kp, d.vp, d.tables, dev_i32(bad), out, None,
+                                       reference_case["n_seq"], reference_case["max_pages"], 16,
+                                       32, 8, 64, 1)
+    finally:
+        llmk.set_check_indices(False)
 
 
 def test_on_a_side_stream(llmk, orc, reference_case):

@@ -586,6 +586,11 @@ def test_engine_rejects_a_pass_over_rows_not_uploaded(llmk):
     e.forward(2)                                       # the rows that were uploaded
     torch.cuda.synchronize()
     assert not torch.isnan(e.logits(2).float()).any()
+
+
+def test_engine_rejects_a_head_dim_other_than_64(llmk):
+    """The attention kernels take head_dim 64 only: a model of another head size is refused when
+    the engine is created."""
     with pytest.raises(llmk.LlmkError) as ei:
         llmk.Engine(llmk.ModelConfig(**dict(TINY, head_dim=128)), 4, 2, 8)
     assert ei.value.status == llmk.LLMK_ERR_SHAPE
