@@ -148,8 +148,8 @@ def test_noalloc_in_a_graph_replayed_with_new_inputs(llmk):
         q_new = torch.from_numpy(
             (rng.uniform(-1, 1, n * NH * HD)).astype(np.float16).view(np.int16)).to(DEV)
         lens_new = np.minimum(lens0, rng.integers(1, 2049, n)).astype(np.int32)
-        case.q.copy_(q_new)
-        case.lens.copy_(torch.from_numpy(lens_new).to(DEV))
+        case.q.view(-1).copy_(q_new)
+        case.lens.view(-1).copy_(torch.from_numpy(lens_new).to(DEV))
         torch.cuda.synchronize()
         out.fill_(0x7F7F)
         g.replay()
