@@ -58,7 +58,8 @@ SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_819
             "pass_floor_stages", "attention_256", "attention_16x2048", "attention_sweep",
             "argmax", "step_256", "step_8", "sched", "probe_sweep", "probe_kernels", "copy_1GiB",
             "residual_add", "rmsnorm_8192", "kv_scatter_8192", "kv_scatter_batch_256",
-            "pass2_graph", "pass2_layers", "pass_fused", "pass2_fused", "end", "setup"]
+            "pass2_graph", "pass2_layers", "pass_fused", "pass2_fused", "calib", "calib_resident",
+            "calib_hbm", "end", "setup"]
 
 # Launch shapes (blocks, threads) of the 16-layer pass at 256 sequences, from the launchers'
 # grid rules: the embedding and add+RMSNorm take one 64-thread wave per row below 4096 rows
@@ -81,14 +82,15 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--kernels", default="all",
                     choices=["all", "kernels", "headline", "configs", "pass", "attn", "probe",
-                             "step", "step8", "sched", "rows"],
+                             "step", "step8", "sched", "rows", "calib"],
                     help="all: everything; kernels: all but the engine step and the scheduler "
                          "(for counter runs); headline: config 2 only; configs: configs 1-4, the "
                          "pass and the probes; pass: the decode pass and its breakdown; attn: decode "
                          "attention and its batch sweep; probe: bandwidth probes; step / step8: "
                          "the engine's decode step of 256 / 8 sequences; sched: the reference's "
                          "scheduler workload; rows: residual_add, RMSNorm [8192,2048] and the "
-                         "two scatters (config 2 is always measured)")
+                         "two scatters; calib: the probes that calibrate the HBM counters "
+                         "(config 2 is always measured)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-seconds", type=float, default=3.0,
                     help="CPU time per configuration (all cores 70%%, one core 30%%)")
@@ -173,6 +175,45 @@ PROFILE_SHAPES = [
 ]
 
 
+# Counter calibration: for each launch shape of PROFILE_SHAPES, a bandwidth probe of the same
+# traffic mix at the same byte count and the same input rotation (so the same share of its data
+# can sit in the 256 MB MALL), run once per counter pass. FETCH_SIZE does not count the bytes
+# read at a fixed ratio: it reads about half of them for data streamed from HBM and about all of
+# them for data the caches hold, so each shape's counters are scaled by what they read for its
+# own probe. (label, probe mode, unit bytes, sets); probe modes as llmk_bw_probe: 0 read,
+# 1 copy (unit read, unit written), 2 read2 (2 units read, one written), 3 in place, 4 write.
+CALIB_PROBES = [
+    ("add_rmsnorm_8192x2048", 1, 67110912, 12),
+    ("residual_add_8192x2048", 2, 33554432, 11),
+    ("rmsnorm_8192x2048", 1, 33556480, 11),
+    ("kv_scatter_8192", 1, 8390656, 64),
+    ("kv_scatter_batch_256", 1, 263168, 16),
+    ("rmsnorm_16x2048", 1, 67584, 8),
+    ("rope_8192", 3, 41959488, 27),
+    ("swiglu_8192x8192", 2, 134217728, 4),
+    ("embedding_8192", 1, 33570816, 16),
+    ("argmax_256x128256", 0, 65668096, 17),
+    ("attention_decode_256", 0, ATTN_BYTES_256, 2),
+    ("attention_decode_16x2048", 0, ATTN_BYTES_16x2048, 17),
+    ("decode:embedding_256", 1, 1049088, 2),
+    ("decode:add_rmsnorm_256x2048", 1, 2099200, 32),
+    ("decode:rope_kv_scatter_256", 1, 1573952, 32),
+    ("decode:swiglu_256x8192", 2, 4194304, 32),
+    ("decode_layers:layer_256", 1, 9964608, 32),
+    ("decode_fused:pass_256", 1, 151569920, 2),
+]
+CALIB_UNROLL = 4
+CALIB_SWEEP_SIZES = (65536, 262144, 1048576, 2097152, 8388608, 33554432)
+PROBE_READS = (1, 1, 2, 1, 0)   # units read per unit of buffer, by probe mode
+PROBE_WRITES = (0, 1, 1, 1, 1)  # units written
+
+
+def _probe_grid(unit: int, unroll: int = CALIB_UNROLL) -> int:
+    """Work-items of a one-pass llmk_bw_probe launch over `unit` bytes."""
+    nvec = unit // 16
+    return -(-nvec // (256 * unroll)) * 256
+
+
 def _name_matches(pattern: str, name: str) -> bool:
     """`pattern`: substrings separated by '|', any of which may occur in the kernel name
     (rocprofv3 prints some names mangled and some demangled)."""
@@ -247,11 +288,45 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
     copy_b = 1 << 30
     sf = copy_b / (avg[ck + ("FETCH_SIZE",)] * 1024)
     sw = copy_b / (avg[ck + ("WRITE_SIZE",)] * 1024)
+
+    def probe_counts(section, mode, unit):
+        pat = f"k_bw_probeILi{mode}ELi{CALIB_UNROLL}E|k_bw_probe<{mode}, {CALIB_UNROLL}>"
+        pk = [k for k in avg if k[0] == section and k[3] == "FETCH_SIZE"
+              and _name_matches(pat, k[1]) and k[2] == _probe_grid(unit)]
+        if not pk:
+            return None
+        base = pk[0][:3]
+        return avg.get(base + ("FETCH_SIZE",)), avg.get(base + ("WRITE_SIZE",))
+
+    print("# Counter calibration: FETCH_SIZE and WRITE_SIZE of a one-pass copy probe (16-byte")
+    print("# non-temporal accesses, 4 per thread) over the bytes read / written, by size; 'resident':")
+    print("# 4 buffers rotated (they stay in the caches between launches), 'hbm': the launches walk")
+    print("# 1 GiB of buffers (every launch reads from HBM). size_kib fetch_ratio write_ratio")
+    for sec in ("calib_resident", "calib_hbm"):
+        for size in CALIB_SWEEP_SIZES:
+            c = probe_counts(sec, 1, size)
+            if c is None or c[0] is None or c[1] is None:
+                print(f"#   {sec:15s} {size >> 10:7d} MISSING")
+                continue
+            print(f"#   {sec:15s} {size >> 10:7d} {c[0] * 1024 / size:7.4f} {c[1] * 1024 / size:7.4f}")
+    print("#")
+    # Per launch shape: the factors of its own probe (same mix, bytes and rotation); the 1 GiB
+    # copy probe's where a shape has none.
+    own = {}
+    for label, mode, unit, _sets in CALIB_PROBES:
+        unit -= unit % 16
+        c = probe_counts("calib", mode, unit)
+        if c is None or not c[0] or not c[1]:
+            continue
+        f_ = PROBE_READS[mode] * unit / (c[0] * 1024) if PROBE_READS[mode] else sf
+        w_ = PROBE_WRITES[mode] * unit / (c[1] * 1024) if PROBE_WRITES[mode] else sw
+        own[label] = (f_, w_)
     print("# Launch shapes. us_mean: mean kernel duration in the kernel trace (all launches of the")
     print("# shape in its section). fetch_kib, write_kib: FETCH_SIZE and WRITE_SIZE per dispatch.")
-    print(f"# traffic_bytes = fetch_kib*1024*{sf:.4f} + write_kib*1024*{sw:.4f}, the factors being")
-    print("# 1 GiB over what each counter reads for the 1 GiB copy probe (1 GiB read and 1 GiB")
-    print("# written per launch).")
+    print("# traffic_bytes = fetch_kib*1024*f + write_kib*1024*w with (f, w) = factor_fetch,")
+    print("# factor_write: bytes read (written) by the shape's own calibration probe over what the")
+    print("# counter reads for it (CALIB_PROBES: same traffic mix, byte count and rotation).")
+    print(f"# traffic_1gib: the same with the 1 GiB copy probe's factors ({sf:.4f}, {sw:.4f}).")
     missing = []
     for label, sec, name, g, alg in PROFILE_SHAPES:
         k = find(sec, name, g)
@@ -264,8 +339,11 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir):
         line = (f"{label} us_mean={sum(d) / len(d):.3f} us_min={min(d):.3f} "
                 f"us_max={max(d):.3f} calls={len(d)}")
         if f is not None and w is not None:
-            traffic = f * 1024 * sf + w * 1024 * sw
-            line += f" fetch_kib={f:.1f} write_kib={w:.1f} traffic_bytes={traffic:.0f}"
+            fs, ws = own.get(label, (sf, sw))
+            traffic = f * 1024 * fs + w * 1024 * ws
+            line += (f" fetch_kib={f:.1f} write_kib={w:.1f} factor_fetch={fs:.4f} "
+                     f"factor_write={ws:.4f} traffic_bytes={traffic:.0f} "
+                     f"traffic_1gib={f * 1024 * sf + w * 1024 * sw:.0f}")
             if alg:
                 line += f" algorithmic_bytes={alg} ratio={traffic / alg:.4f}"
         print(line)
@@ -1126,6 +1204,50 @@ class Bench:
             self.free()
         return out
 
+    def calibration(self):
+        """Probes whose counters scale each launch shape's FETCH_SIZE / WRITE_SIZE: a copy probe
+        swept over CALIB_SWEEP_SIZES with the buffers cache-resident and with every launch on
+        fresh HBM, and one probe per CALIB_PROBES entry (the shape's mix, bytes and rotation).
+        A few launches each: only their counters are used."""
+        llmk, torch = self.llmk, self.torch
+        big = 1 << 30
+        src = torch.empty(big, dtype=torch.uint8, device=self.dev)
+        dst = torch.empty(big, dtype=torch.uint8, device=self.dev)
+        src.random_(0, 256)
+        for sec, resident in (("calib_resident", True), ("calib_hbm", False)):
+            self.mark(sec)
+            for size in CALIB_SWEEP_SIZES:
+                slots = 4 if resident else big // size
+                for i in range(24):
+                    o = (i % slots) * size
+                    llmk.bw_probe(1, dst[o:o + size], size, a=src[o:o + size], blocks=0,
+                                  unroll=CALIB_UNROLL)
+                torch.cuda.synchronize()
+        del src, dst
+        self.free()
+        self.mark("calib")
+        for label, mode, unit, R in CALIB_PROBES:
+            unit -= unit % 16
+            n_in = 2 if mode == 2 else (0 if mode in (3, 4) else 1)
+            bufs = [[torch.empty(unit, dtype=torch.uint8, device=self.dev)
+                     for _ in range(n_in + (1 if mode != 0 else 0))] for _ in range(R)]
+            for st in bufs:
+                for t in st:
+                    t.random_(0, 256)
+            for i in range(3 + 20):
+                st = bufs[i % R]
+                if mode == 0:
+                    llmk.bw_probe(0, st[0], unit, a=st[0], unroll=CALIB_UNROLL)
+                elif mode == 1:
+                    llmk.bw_probe(1, st[1], unit, a=st[0], unroll=CALIB_UNROLL)
+                elif mode == 2:
+                    llmk.bw_probe(2, st[2], unit, a=st[0], b=st[1], unroll=CALIB_UNROLL)
+                else:
+                    llmk.bw_probe(mode, st[0], unit, unroll=CALIB_UNROLL)
+            torch.cuda.synchronize()
+            del bufs
+            self.free()
+
     def copy_probe(self):
         llmk, torch = self.llmk, self.torch
         nb = 1 << 30
@@ -1420,6 +1542,46 @@ class Bench:
             raise RuntimeError("batched and one-at-a-time scheduler outputs differ")
         best = {mr: max(r["words_per_s"] for r in rounds if r["max_running"] == mr)
                 for mr in (1, wl.SCHED_MAX_RUNNING)}
+
+        # The reference's A/B of where the greedy choice is made (tests/test_scheduler_ab.cu):
+        # all 24 requests eligible at once, up to 8 at once and one at a time, the argmax on the
+        # host (the reference's default: logits copied back, converted, searched) and on the
+        # GPU; three rounds, the order of the four reversed every other round; per decode step
+        # the time split of llmk_step_times (ref: engine/batched.h:6-11).
+        ab_reqs = [dict(r, arrival_step=0) for r in reqs]
+        cfgs = [("batched, CPU argmax", wl.SCHED_MAX_RUNNING, 1),
+                ("batched, GPU argmax", wl.SCHED_MAX_RUNNING, 0),
+                ("one at a time, CPU argmax", 1, 1), ("one at a time, GPU argmax", 1, 0)]
+        for host in (1, 0):  # warm-up of both paths (and their graphs), as the reference's
+            eng.set_option(llmk.ENGINE_HOST_ARGMAX, host)
+            run(ab_reqs[:2], wl.SCHED_MAX_RUNNING)
+            run(ab_reqs[:wl.SCHED_MAX_RUNNING], wl.SCHED_MAX_RUNNING)
+        ab_rounds, ab_outs = [], None
+        for rnd in (1, 2, 3):
+            for k in range(4):
+                name, mr, host = cfgs[k if rnd % 2 else 3 - k]
+                eng.set_option(llmk.ENGINE_HOST_ARGMAX, host)
+                outs, st = run(ab_reqs, mr)
+                if ab_outs is None:
+                    ab_outs = outs
+                elif outs != ab_outs:
+                    raise RuntimeError(f"scheduler A/B: outputs of '{name}' differ")
+                steps = max(1, st["decode_steps"])
+                wps = st["total_words"] / (st["total_ms"] * 1e-3)
+                per = {key: round(st[key + "_ms"] / steps, 4)
+                       for key in ("prep", "gpu", "copy", "convert", "argmax")}
+                ab_rounds.append({"round": rnd, "config": name, "words_per_s": round(wps, 1),
+                                  "decode_steps": st["decode_steps"],
+                                  "prefill_ms": round(st["prefill_ms"], 2),
+                                  "per_step_ms": per})
+                log(f"  scheduler A/B round {rnd} | {name:26s} | {wps:6.0f} words/s | "
+                    f"{st['decode_steps']:3d} steps | prefill {st['prefill_ms']:6.1f} ms | per "
+                    f"step (ms): " + ", ".join(f"{k_} {v:.3f}" for k_, v in per.items()))
+        eng.set_option(llmk.ENGINE_HOST_ARGMAX, 0)
+        med = {}
+        for name, _, _ in cfgs:
+            v = sorted(r["words_per_s"] for r in ab_rounds if r["config"] == name)
+            med[name] = v[len(v) // 2]
         eng.close()
         self.free()
         self.kernels["scheduler_24x32_1b"] = {
@@ -1427,7 +1589,17 @@ class Bench:
             "words_per_s": best[wl.SCHED_MAX_RUNNING], "words_per_s_one_at_a_time": best[1],
             "gain": round(best[wl.SCHED_MAX_RUNNING] / best[1], 2), "rounds": rounds,
             "note": "reference on an RTX 4050 Laptop: 249 words/s up to 8 at once, 60 one at a "
-                    "time (docs/scheduler_results.md); outputs identical in both modes"}
+                    "time (docs/scheduler_results.md); outputs identical in both modes",
+            "argmax_ab": {
+                "median_words_per_s": med,
+                "gpu_over_cpu_argmax": {
+                    "batched": round(med["batched, GPU argmax"] / med["batched, CPU argmax"], 3),
+                    "one_at_a_time": round(med["one at a time, GPU argmax"]
+                                           / med["one at a time, CPU argmax"], 3)},
+                "rounds": ab_rounds,
+                "note": "all 24 requests eligible at once (ref: tests/test_scheduler_ab.cu); "
+                        "outputs identical in all four configurations; reference on an RTX 4050 "
+                        "Laptop: 291 / 291 / 64 / 68 words/s (docs/step_time_split_results.txt)"}}
 
 
 def cpu_model() -> str:
@@ -1533,6 +1705,8 @@ def main() -> int:
     if allk or what in ("probe", "configs"):
         sweep = b.probes()
         b.kernel_ceilings(sweep)
+    if allk or what == "calib":
+        b.calibration()
     b.copy_probe()
     b.mark("end")
     torch.cuda.synchronize()

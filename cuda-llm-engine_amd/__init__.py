@@ -133,14 +133,22 @@ class SchedStats(ctypes.Structure):
     """Mirror of ``struct llmk_sched_stats`` (ref: engine/scheduler.h:16-22)."""
     _fields_ = [("decode_steps", _i), ("total_words", _i), ("prefills", _i), ("max_batch", _i),
                 ("iterations", _i), ("total_ms", _d), ("mean_batch", _d), ("prefill_ms", _d),
-                ("decode_ms", _d)]
+                ("decode_ms", _d), ("prep_ms", _d), ("gpu_ms", _d), ("copy_ms", _d),
+                ("convert_ms", _d), ("argmax_ms", _d)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
 
 
 PREFILL_FN = ctypes.CFUNCTYPE(_i, _vp, _i32p, _i, _i32p, _i, _i32p)
-DECODE_FN = ctypes.CFUNCTYPE(_i, _vp, _i, _i32p, _i32p, _i32p, _i, _i32p)
+class StepTimes(ctypes.Structure):
+    """Mirror of ``struct llmk_step_times`` (ref: engine/batched.h:6-11 StepTimes)."""
+    _fields_ = [("prep_ms", _d), ("gpu_ms", _d), ("copy_ms", _d), ("convert_ms", _d),
+                ("argmax_ms", _d)]
+
+
+DECODE_FN = ctypes.CFUNCTYPE(_i, _vp, _i, _i32p, _i32p, _i32p, _i, _i32p,
+                             ctypes.POINTER(StepTimes))
 
 
 class SchedModel(ctypes.Structure):
@@ -637,6 +645,7 @@ def linear(handle: Blas, x, w, y, T: int, in_features: int, out_features: int,
 
 LINEAR_ROWS_MAX = 8  # LLMK_LINEAR_ROWS_MAX
 ENGINE_FUSE_FEW_ROWS = 1  # LLMK_ENGINE_FUSE_FEW_ROWS
+ENGINE_HOST_ARGMAX = 2  # LLMK_ENGINE_HOST_ARGMAX
 
 
 def linear_rows(x, w, y, T: int, in_features: int, out_features: int, stream=None) -> None:
@@ -882,7 +891,7 @@ class Engine:
         _check("engine_reset_pools", _lib.llmk_engine_reset_pools(self._e, _stream(stream)))
 
     def set_option(self, option: int, value: int) -> None:
-        """``llmk_engine_set_option`` (ENGINE_FUSE_FEW_ROWS)."""
+        """``llmk_engine_set_option`` (ENGINE_FUSE_FEW_ROWS, ENGINE_HOST_ARGMAX)."""
         _check("engine_set_option", _lib.llmk_engine_set_option(self._e, option, value))
 
     def buffer_ptr(self, which: int, layer: int = 0) -> int:
@@ -990,7 +999,7 @@ def python_sched_model(prefill, decode) -> SchedModel:
             m._errors.append(exc)
             return LLMK_ERR_INVALID_VALUE
 
-    def _decode(user, n, tokens, positions, tables, max_pages, out):
+    def _decode(user, n, tokens, positions, tables, max_pages, out, times):
         try:
             tok = np.ctypeslib.as_array(tokens, (n,)).copy()
             pos = np.ctypeslib.as_array(positions, (n,)).copy()

@@ -35,6 +35,7 @@
 #include <string.h>
 #include <unistd.h>
 
+#include <chrono>
 #include <map>
 #include <string>
 #include <tuple>
@@ -94,14 +95,21 @@ struct llmk_engine {
   // since the device copies past them hold no checked indices.
   int rows_set = 0, logit_rows_set = 0;
 
-  // HIP graphs of the forward pass, keyed by (n_rows, n_logit_rows, resolved num_splits)
+  // HIP graphs of the forward pass, keyed by (n_rows, n_logit_rows, resolved num_splits,
+  // host_argmax: whether the pass ends before the GPU argmax)
   struct Graph {
     bool seen = false;
     hipGraphExec_t exec = nullptr;
   };
-  std::map<std::tuple<int, int, int>, Graph> graphs;
+  std::map<std::tuple<int, int, int, int>, Graph> graphs;
   hipStream_t sched_stream = nullptr;  // the stream the scheduler callbacks run on
   bool fuse_rows = true;  // passes of <= LLMK_LINEAR_ROWS_MAX rows use the fused projections
+  // LLMK_ENGINE_HOST_ARGMAX: the pass ends with the logits; the scheduler callbacks copy them
+  // to host_logits (pinned, max_rows rows), convert them into host_float and pick there.
+  bool host_argmax = false;
+  uint16_t* host_logits = nullptr;
+  std::vector<float> host_float;
+  hipEvent_t step_begin = nullptr, step_end = nullptr;  // a decode step's GPU time
 };
 
 namespace {
@@ -184,6 +192,9 @@ void release(llmk_engine* e) {
   if (e->act_buf) (void)hipFree(e->act_buf);
   if (e->staging) (void)hipHostFree(e->staging);
   if (e->staged) (void)hipEventDestroy(e->staged);
+  if (e->host_logits) (void)hipHostFree(e->host_logits);
+  if (e->step_begin) (void)hipEventDestroy(e->step_begin);
+  if (e->step_end) (void)hipEventDestroy(e->step_end);
   delete e;
 }
 
@@ -220,6 +231,8 @@ extern "C" int llmk_engine_create(const llmk_model_config* cfg, int max_rows, in
   if (st == LLMK_OK) st = (int)hipHostMalloc(&e->staging, ci.off, hipHostMallocDefault);
   if (st == LLMK_OK) memset(e->staging, 0, ci.off);  // every upload copies all of it
   if (st == LLMK_OK) st = (int)hipEventCreateWithFlags(&e->staged, hipEventDisableTiming);
+  if (st == LLMK_OK) st = (int)hipEventCreate(&e->step_begin);
+  if (st == LLMK_OK) st = (int)hipEventCreate(&e->step_end);
   if (st == LLMK_OK) st = llmk_blas_create(&e->blas);
   if (st != LLMK_OK) {
     release(e);
@@ -518,7 +531,7 @@ static int forward_fused_rows(llmk_engine* e, int n, int nl, bool all_rows, int 
     LLMK_TRY(llmk_linear_rows_norm(lm_in, e->final_norm, m.eps, e->embed, e->logits, nl, H,
                                    m.vocab, s));
   }
-  LLMK_TRY(llmk_argmax_rows(e->logits, e->next, nl, m.vocab, s));
+  if (!e->host_argmax) LLMK_TRY(llmk_argmax_rows(e->logits, e->next, nl, m.vocab, s));
 #undef LLMK_TRY
   return LLMK_OK;
 }
@@ -534,6 +547,19 @@ extern "C" int llmk_engine_set_option(llmk_engine* e, int option, int value) {
         e->graphs.clear();
       }
       e->fuse_rows = value != 0;
+      return LLMK_OK;
+    case LLMK_ENGINE_HOST_ARGMAX:
+      if (value != 0 && !e->host_logits) {
+        const size_t rows = (size_t)e->max_rows * e->cfg.vocab;
+        const int st = (int)hipHostMalloc(reinterpret_cast<void**>(&e->host_logits),
+                                          rows * sizeof(uint16_t), hipHostMallocDefault);
+        if (st != LLMK_OK) {
+          e->host_logits = nullptr;
+          return st;
+        }
+        e->host_float.resize(rows);
+      }
+      e->host_argmax = value != 0;  // the graph cache keys the two kinds of pass apart
       return LLMK_OK;
     default:
       return LLMK_ERR_INVALID_VALUE;
@@ -600,7 +626,7 @@ extern "C" int llmk_engine_forward(llmk_engine* e, int n_rows, int n_logit_rows,
     return LLMK_OK;
   }
   LLMK_TRY(llmk_linear(e->blas, lm_in, e->embed, e->logits, nl, H, m.vocab, s));
-  LLMK_TRY(llmk_argmax_rows(e->logits, e->next, nl, m.vocab, s));
+  if (!e->host_argmax) LLMK_TRY(llmk_argmax_rows(e->logits, e->next, nl, m.vocab, s));
 #undef LLMK_TRY
   return LLMK_OK;
 }
@@ -638,7 +664,7 @@ extern "C" int llmk_engine_forward_graph(llmk_engine* e, int n_rows, int n_logit
   if (!rows_uploaded(e, n_rows, n_logit_rows)) return LLMK_ERR_INVALID_VALUE;
   num_splits = resolve_splits(e, n_rows, num_splits);  // the key holds the launch shapes
   llmk_engine::Graph& g = e->graphs[std::make_tuple(n_rows, n_logit_rows < 0 ? -1 : n_logit_rows,
-                                                    num_splits)];
+                                                    num_splits, e->host_argmax ? 1 : 0)];
   if (g.exec) return (int)hipGraphLaunch(g.exec, s);
   if (!g.seen) {  // first use: eager, which also makes the GEMM plans of these shapes
     g.seen = true;
@@ -667,11 +693,50 @@ extern "C" int llmk_engine_forward_graph(llmk_engine* e, int n_rows, int n_logit
 // ---------------------------------------------------------------------------------------------
 namespace {
 
+using Clock = std::chrono::steady_clock;
+
+double ms_since(Clock::time_point t) {
+  return std::chrono::duration<double, std::milli>(Clock::now() - t).count();
+}
+
 int read_tokens(llmk_engine* e, int32_t* dst, int n) {
   int st = (int)hipMemcpyAsync(dst, e->next, (size_t)n * sizeof(int32_t), hipMemcpyDeviceToHost,
                                e->sched_stream);
   if (st == LLMK_OK) st = (int)hipStreamSynchronize(e->sched_stream);
   return st;
+}
+
+// The reference's host argmax (engine/scheduler.cu:9-13): the first index holding the row's
+// maximum; comparisons with NaN are false, so a NaN never replaces the running best.
+int host_argmax_row(const float* lg, int vocab) {
+  int best = 0;
+  for (int v = 1; v < vocab; ++v)
+    if (lg[v] > lg[best]) best = v;
+  return best;
+}
+
+// Host-argmax mode: copies the n logit rows back (copy_ms), converts them to float
+// (convert_ms) and picks each row's token (argmax_ms); ref: engine/batched.cu:126-139,
+// engine/scheduler.cu:88-93.
+int host_pick(llmk_engine* e, int n, int32_t* out, llmk_step_times* times) {
+  const size_t count = (size_t)n * e->cfg.vocab;
+  const auto t0 = Clock::now();
+  int st = (int)hipMemcpyAsync(e->host_logits, e->logits, count * sizeof(uint16_t),
+                               hipMemcpyDeviceToHost, e->sched_stream);
+  if (st == LLMK_OK) st = (int)hipStreamSynchronize(e->sched_stream);
+  if (st != LLMK_OK) return st;
+  const auto t1 = Clock::now();
+  for (size_t i = 0; i < count; ++i)
+    e->host_float[i] = (float)__builtin_bit_cast(_Float16, e->host_logits[i]);
+  const auto t2 = Clock::now();
+  for (int r = 0; r < n; ++r)
+    out[r] = host_argmax_row(e->host_float.data() + (size_t)r * e->cfg.vocab, e->cfg.vocab);
+  if (times) {
+    times->copy_ms += std::chrono::duration<double, std::milli>(t1 - t0).count();
+    times->convert_ms += std::chrono::duration<double, std::milli>(t2 - t1).count();
+    times->argmax_ms += ms_since(t2);
+  }
+  return LLMK_OK;
 }
 
 // A prompt as rows at positions 0 .. len-1, in chunks of at most max_rows rows; only the last
@@ -697,20 +762,41 @@ int sched_prefill(void* user, const int32_t* table, int max_pages, const int32_t
     if (st == LLMK_OK) st = llmk_engine_forward(e, n, last ? 1 : 0, 0, e->sched_stream);
     if (st != LLMK_OK) return st;
   }
-  return read_tokens(e, next_token, 1);
+  return e->host_argmax ? host_pick(e, 1, next_token, nullptr) : read_tokens(e, next_token, 1);
 }
 
+// One decode step with the reference's time split (engine/batched.cu:90-150): prep = the rows'
+// host preparation and upload, gpu = events around the pass, then the copy back and, in
+// host-argmax mode, the conversion and the search.
 int sched_decode(void* user, int n, const int32_t* tokens, const int32_t* positions,
-                 const int32_t* tables, int max_pages, int32_t* next_tokens) {
+                 const int32_t* tables, int max_pages, int32_t* next_tokens,
+                 llmk_step_times* times) {
   llmk_engine* e = static_cast<llmk_engine*>(user);
   if (n <= 0 || n > e->max_rows || max_pages != e->max_pages || !next_tokens)
     return LLMK_ERR_INVALID_VALUE;
+  const auto t0 = Clock::now();
   int st = llmk_engine_set_rows(e, n, tokens, positions, tables, 0, nullptr, e->sched_stream);
+  if (st != LLMK_OK) return st;
+  const double prep = ms_since(t0);
+  st = (int)hipEventRecord(e->step_begin, e->sched_stream);
   if (st != LLMK_OK) return st;
   st = e->sched_stream ? llmk_engine_forward_graph(e, n, -1, 0, e->sched_stream)
                        : llmk_engine_forward(e, n, -1, 0, e->sched_stream);
   if (st != LLMK_OK) return st;
-  return read_tokens(e, next_tokens, n);
+  st = (int)hipEventRecord(e->step_end, e->sched_stream);
+  if (st == LLMK_OK) st = (int)hipEventSynchronize(e->step_end);
+  float gpu = 0.0f;
+  if (st == LLMK_OK) st = (int)hipEventElapsedTime(&gpu, e->step_begin, e->step_end);
+  if (st != LLMK_OK) return st;
+  if (times) {
+    times->prep_ms += prep;
+    times->gpu_ms += gpu;
+  }
+  if (e->host_argmax) return host_pick(e, n, next_tokens, times);
+  const auto t2 = Clock::now();
+  st = read_tokens(e, next_tokens, n);
+  if (st == LLMK_OK && times) times->copy_ms += ms_since(t2);
+  return st;
 }
 
 }  // namespace

@@ -436,7 +436,8 @@ LLMK_API int llmk_engine_set_rows(llmk_engine* e, int n_rows, const int32_t* tok
 
 /* Enqueues the forward pass over the first n_rows uploaded rows: embedding, every layer (K and
  * V of each row written to the pools), final norm, logits [nl, vocab] and their argmax [nl]
- * (nl = n_rows if n_logit_rows < 0, else the uploaded logit rows). n_rows may not exceed the
+ * (nl = n_rows if n_logit_rows < 0, else the uploaded logit rows; no argmax with the option
+ * LLMK_ENGINE_HOST_ARGMAX set). n_rows may not exceed the
  * rows of the last llmk_engine_set_rows, nor n_logit_rows its logit rows
  * (LLMK_ERR_INVALID_VALUE before any launch): only those rows' indices were checked.
  * num_splits <= 0 picks the split count: 1 when every uploaded row's attention reads at most 4
@@ -466,6 +467,13 @@ LLMK_API int llmk_engine_reset_pools(llmk_engine* e, void* stream);
  * give the bits of the unfused pass in 6 launches per layer instead of 10; 0 runs the unfused
  * pass. Changing it drops the cached graphs. New entry point. */
 #define LLMK_ENGINE_FUSE_FEW_ROWS 1
+/* LLMK_ENGINE_HOST_ARGMAX (default 0): 1 leaves the greedy choice to the host. The forward pass
+ * then ends with the logits (LLMK_BUF_NEXT_TOKENS is not written), and the scheduler callbacks
+ * (llmk_engine_sched_model) copy them back and pick each row's token on the host, as the
+ * reference's scheduler does without gpu_argmax. Setting it allocates the pinned host copy of
+ * max_rows logit rows (a hipError_t status on failure); the graph cache of
+ * llmk_engine_forward_graph keeps the passes of both settings apart. */
+#define LLMK_ENGINE_HOST_ARGMAX 2
 LLMK_API int llmk_engine_set_option(llmk_engine* e, int option, int value);
 
 /* Tunes the GEMM plans of a forward pass over n_rows rows with n_logit_rows logit rows (< 0:
@@ -475,7 +483,8 @@ LLMK_API int llmk_engine_set_option(llmk_engine* e, int option, int value);
 LLMK_API int llmk_engine_tune(llmk_engine* e, int n_rows, int n_logit_rows, void* stream);
 
 /* llmk_engine_forward through a HIP graph cache keyed by (n_rows, n_logit_rows, the resolved
- * split count -- num_splits <= 0 resolved against the rows last uploaded, as above):
+ * split count -- num_splits <= 0 resolved against the rows last uploaded, as above -- and the
+ * LLMK_ENGINE_HOST_ARGMAX setting):
  * the first call of a key runs eagerly (choosing the GEMM plans), the second captures the pass
  * on `stream` and instantiates it, later calls launch the instance. Same results as
  * llmk_engine_forward. `stream` must not be the null stream (it cannot be captured) and must
@@ -517,22 +526,39 @@ typedef struct llmk_request {
   double t_arrive_ms, t_first_ms, t_done_ms;
 } llmk_request;
 
-/* Totals of one run (ref: engine/scheduler.h:16-22 SchedulerStats). */
+/* One decode step's time split, milliseconds (ref: engine/batched.h:6-11 StepTimes):
+ * prep_ms host-side batch preparation and uploads; gpu_ms GPU time from the step's first kernel
+ * to its last (events); copy_ms the copy of the results back to the host (the chosen tokens, or
+ * the logits in host-argmax mode); convert_ms the half -> float conversion of the logits on the
+ * host, and argmax_ms the host argmax over them (host-argmax mode only; the reference's
+ * scheduler times that argmax, engine/scheduler.cu:88-93). A decode callback adds its step's
+ * times to the fields (they start at 0). */
+typedef struct llmk_step_times {
+  double prep_ms, gpu_ms, copy_ms, convert_ms, argmax_ms;
+} llmk_step_times;
+
+/* Totals of one run (ref: engine/scheduler.h:16-22 SchedulerStats): decode_ms is the
+ * host-observed time of the decode steps, and prep_ms .. argmax_ms sum the steps'
+ * llmk_step_times, as the reference's time split does. */
 typedef struct llmk_sched_stats {
   int decode_steps, total_words, prefills, max_batch, iterations;
   double total_ms, mean_batch, prefill_ms, decode_ms;
+  double prep_ms, gpu_ms, copy_ms, convert_ms, argmax_ms;
 } llmk_sched_stats;
 
 /* The model as the scheduler sees it. prefill: run prompt[0 .. len) at positions 0 .. len-1 of
  * the sequence whose block table is table[max_pages], write the greedy next token. decode: run
  * n rows (tokens[i] at positions[i] of the sequence with table row i of tables[n, max_pages]),
- * write the n greedy next tokens. Both return LLMK_OK or an error code, which ends the run. */
+ * write the n greedy next tokens, and add the step's time split to *times (never NULL; a model
+ * that does not measure leaves it alone). Both return LLMK_OK or an error code, which ends the
+ * run. */
 typedef struct llmk_sched_model {
   void* user;
   int (*prefill)(void* user, const int32_t* table, int max_pages, const int32_t* prompt, int len,
                  int32_t* next_token);
   int (*decode)(void* user, int n, const int32_t* tokens, const int32_t* positions,
-                const int32_t* tables, int max_pages, int32_t* next_tokens);
+                const int32_t* tables, int max_pages, int32_t* next_tokens,
+                llmk_step_times* times);
 } llmk_sched_model;
 
 /* Runs every request to completion with continuous batching: arrivals by iteration, at most one
@@ -548,9 +574,13 @@ LLMK_API int llmk_scheduler_run(llmk_request* reqs, int n_reqs, int max_running,
                                 const llmk_sched_model* model, llmk_sched_stats* stats);
 
 /* Scheduler callbacks that run the engine on `stream` (not the null stream): prefill in chunks
- * of at most max_rows rows (eager), decode through llmk_engine_forward_graph; the greedy tokens
- * come from the engine's GPU argmax (the reference's gpu_argmax mode,
- * ref: engine/batched.cu:146-150). The engine's block tables must have the same max_pages. */
+ * of at most max_rows rows (eager), decode through llmk_engine_forward_graph, each step's time
+ * split measured as the reference measures it (engine/batched.cu:90-150). The greedy tokens come
+ * from the engine's GPU argmax (the reference's gpu_argmax mode, ref: engine/batched.cu:146-150),
+ * or, with the engine option LLMK_ENGINE_HOST_ARGMAX set, from the logits copied to the host,
+ * converted to float and searched there with the reference's rule (the first maximum wins;
+ * ref: engine/scheduler.cu:9-13,88-93, engine/batched.cu:126-139), for prompts as well. The
+ * engine's block tables must have the same max_pages. */
 LLMK_API int llmk_engine_sched_model(llmk_engine* e, void* stream, llmk_sched_model* out);
 
 #ifdef __cplusplus

@@ -161,19 +161,26 @@ struct Request {
   double t_arrive_ms = -1, t_first_ms = -1, t_done_ms = -1;
 };
 
-// ref: engine/scheduler.h:16-22 (decode_ms: the host-observed time of the decode steps)
+// ref: engine/scheduler.h:16-22 (decode_ms: the host-observed time of the decode steps; the
+// time split summed over the decode steps, as the reference's)
 struct SchedulerStats {
   int decode_steps = 0;
   int total_words = 0;
   double total_ms = 0, mean_batch = 0;
   double prefill_ms = 0, decode_ms = 0;
+  double prep_ms = 0, gpu_ms = 0, copy_ms = 0, convert_ms = 0, argmax_ms = 0;
 };
 
-// ref: engine/scheduler.h:24-27, engine/scheduler.cu:15-106. Greedy tokens come from the
-// engine's GPU argmax (the reference's gpu_argmax mode). `stream` should be a created stream:
-// decode steps then replay HIP graphs.
+// ref: engine/scheduler.h:24-27, engine/scheduler.cu:15-106. gpu_argmax (the reference's
+// parameter, same default): the greedy tokens come from the engine's GPU argmax; otherwise the
+// logits are copied back and searched on the host (LLMK_ENGINE_HOST_ARGMAX, left set as chosen
+// here). `stream` should be a created stream: decode steps then replay HIP graphs.
 inline SchedulerStats run_scheduler(Engine& e, PageAllocator& pages, std::vector<Request>& reqs,
-                                    int max_running, hipStream_t stream) {
+                                    int max_running, hipStream_t stream,
+                                    bool gpu_argmax = false) {
+  llmk_shim_engine::check(llmk_engine_set_option(e.get(), LLMK_ENGINE_HOST_ARGMAX,
+                                                 gpu_argmax ? 0 : 1),
+                          "run_scheduler");
   std::vector<llmk_request> rq(reqs.size());
   for (size_t i = 0; i < reqs.size(); ++i) {
     reqs[i].output.assign(reqs[i].max_new > 0 ? reqs[i].max_new : 1, 0);
@@ -203,6 +210,11 @@ inline SchedulerStats run_scheduler(Engine& e, PageAllocator& pages, std::vector
   out.mean_batch = st.mean_batch;
   out.prefill_ms = st.prefill_ms;
   out.decode_ms = st.decode_ms;
+  out.prep_ms = st.prep_ms;
+  out.gpu_ms = st.gpu_ms;
+  out.copy_ms = st.copy_ms;
+  out.convert_ms = st.convert_ms;
+  out.argmax_ms = st.argmax_ms;
   return out;
 }
 

@@ -436,21 +436,37 @@ int main() {
     }
     hipStream_t stream;
     HIP_CHECK(hipStreamCreate(&stream));
-    std::vector<llmk::Request> one = base, three = base;
+    std::vector<llmk::Request> one = base, three = base, three_gpu = base;
     llmk::PageAllocator pages(num_pages);
+    // the reference's default: the greedy choice on the host
     const llmk::SchedulerStats s1 = llmk::run_scheduler(eng, pages, one, 1, stream);
     const int free1 = pages.num_free();
     const llmk::SchedulerStats s3 = llmk::run_scheduler(eng, pages, three, 3, stream);
-    bool same = true;
-    for (int i = 0; i < 9; ++i)
+    const llmk::SchedulerStats g3 =
+        llmk::run_scheduler(eng, pages, three_gpu, 3, stream, /*gpu_argmax=*/true);
+    bool same = true, same_gpu = true;
+    for (int i = 0; i < 9; ++i) {
       same = same && one[i].output == three[i].output &&
              (int)one[i].output.size() == base[i].max_new;
+      same_gpu = same_gpu && three_gpu[i].output == three[i].output;
+    }
     std::snprintf(detail, sizeof(detail), "(%d vs %d decode steps)", s1.decode_steps,
                   s3.decode_steps);
     report("run_scheduler: batched outputs = one at a time", same, detail);
+    report("run_scheduler: GPU argmax = host argmax", same_gpu);
     report("run_scheduler: batching takes fewer steps", s3.decode_steps < s1.decode_steps);
     report("run_scheduler: every page returned", free1 == num_pages &&
                                                      pages.num_free() == num_pages);
+    std::snprintf(detail, sizeof(detail),
+                  "(host: prep %.2f gpu %.2f copy %.2f convert %.2f argmax %.2f ms; gpu mode: "
+                  "convert %.2f argmax %.2f)",
+                  s3.prep_ms, s3.gpu_ms, s3.copy_ms, s3.convert_ms, s3.argmax_ms, g3.convert_ms,
+                  g3.argmax_ms);
+    report("run_scheduler: time split filled in",
+           s3.gpu_ms > 0 && s3.copy_ms > 0 && s3.convert_ms > 0 && s3.argmax_ms > 0 &&
+               s3.prep_ms > 0 && g3.gpu_ms > 0 && g3.copy_ms > 0 && g3.convert_ms == 0 &&
+               g3.argmax_ms == 0 && s3.gpu_ms <= s3.decode_ms && g3.gpu_ms <= g3.decode_ms,
+           detail);
     HIP_CHECK(hipStreamDestroy(stream));
   }
 

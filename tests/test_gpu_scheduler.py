@@ -69,3 +69,44 @@ def test_scheduler_with_the_engine(llmk, orc):
     assert results[4][0] == o_outs
     assert results[4][1]["decode_steps"] == o_stats["decode_steps"]
     assert sorted(o_free) == list(range(num_pages))
+
+
+def test_scheduler_host_argmax_mode(llmk):
+    """The reference's default mode (run_scheduler without gpu_argmax): the logits come back to
+    the host, are converted to float there and searched with its rule (first maximum wins;
+    ref: engine/scheduler.cu:9-13,88-93). The same workload gives the same tokens as the GPU
+    argmax, one at a time and batched, and the time split is filled in as the reference fills
+    it: prep, GPU, copy, convert and argmax in host mode; convert and argmax stay 0 in GPU
+    mode, and the GPU time of the steps never exceeds their host-observed time."""
+    w = tiny_weights(0x5EED0410, embed_std=0.5)
+    num_pages, max_pages, max_rows = 48, 8, 16
+    eng = make_engine(llmk, TINY, w, max_rows, max_pages, num_pages)
+    stream = torch.cuda.Stream()
+    model = eng.sched_model(stream)
+    reqs = workload(0x5EED0411)
+    order = np.random.default_rng(0x5EED0412).permutation(num_pages).astype(np.int32)
+
+    def run(max_running):
+        pages = llmk.PageAllocator(num_pages)
+        pages.set_free_list(order)
+        outs, stats, _ = llmk.run_scheduler(reqs, max_running, max_pages, P, pages, model)
+        assert pages.num_free() == num_pages
+        return outs, stats
+
+    gpu = {mr: run(mr) for mr in (1, 4)}
+    eng.set_option(llmk.ENGINE_HOST_ARGMAX, 1)
+    host = {mr: run(mr) for mr in (1, 4)}
+    eng.set_option(llmk.ENGINE_HOST_ARGMAX, 0)
+    again = run(4)
+    for mr in (1, 4):
+        assert host[mr][0] == gpu[mr][0], mr
+        h, g = host[mr][1], gpu[mr][1]
+        print(f"max_running {mr}: host {h}\n  gpu {g}", flush=True)
+        assert h["decode_steps"] == g["decode_steps"]
+        for key in ("prep_ms", "gpu_ms", "copy_ms", "convert_ms", "argmax_ms"):
+            assert h[key] > 0, key
+        for key in ("prep_ms", "gpu_ms", "copy_ms"):
+            assert g[key] > 0, key
+        assert g["convert_ms"] == 0 and g["argmax_ms"] == 0
+        assert h["gpu_ms"] <= h["decode_ms"] and g["gpu_ms"] <= g["decode_ms"]
+    assert again[0] == gpu[4][0]
