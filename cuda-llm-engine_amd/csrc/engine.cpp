@@ -707,12 +707,29 @@ int read_tokens(llmk_engine* e, int32_t* dst, int n) {
 }
 
 // The reference's host argmax (engine/scheduler.cu:9-13): the first index holding the row's
-// maximum; comparisons with NaN are false, so a NaN never replaces the running best.
+// maximum; comparisons with NaN are false, so a NaN never replaces the running best (and a NaN
+// at index 0 is never replaced). The running best value is kept rather than re-read.
 int host_argmax_row(const float* lg, int vocab) {
   int best = 0;
+  float bv = lg[0];
   for (int v = 1; v < vocab; ++v)
-    if (lg[v] > lg[best]) best = v;
+    if (lg[v] > bv) {
+      bv = lg[v];
+      best = v;
+    }
   return best;
+}
+
+// fp16 -> fp32, exact and branch-free: the magnitude bits moved into place read as a float
+// 2^112 too small for normal numbers and as the float subnormal m * 2^-136 for fp16 subnormals
+// (value m * 2^-24); the product with 2^112 is exact in both cases. Inf and NaN keep their
+// mantissa under an all-ones exponent. (The reference converts with __half2float on the host,
+// engine/batched.cu:135.)
+inline float half_to_float(uint16_t h) {
+  const uint32_t em = h & 0x7FFFu;
+  float f = __builtin_bit_cast(float, em << 13) * 0x1.0p112f;
+  if (em >= 0x7C00u) f = __builtin_bit_cast(float, (em << 13) | 0x7F800000u);
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, f) | ((uint32_t)(h & 0x8000u) << 16));
 }
 
 // Host-argmax mode: copies the n logit rows back (copy_ms), converts them to float
@@ -726,8 +743,7 @@ int host_pick(llmk_engine* e, int n, int32_t* out, llmk_step_times* times) {
   if (st == LLMK_OK) st = (int)hipStreamSynchronize(e->sched_stream);
   if (st != LLMK_OK) return st;
   const auto t1 = Clock::now();
-  for (size_t i = 0; i < count; ++i)
-    e->host_float[i] = (float)__builtin_bit_cast(_Float16, e->host_logits[i]);
+  for (size_t i = 0; i < count; ++i) e->host_float[i] = half_to_float(e->host_logits[i]);
   const auto t2 = Clock::now();
   for (int r = 0; r < n; ++r)
     out[r] = host_argmax_row(e->host_float.data() + (size_t)r * e->cfg.vocab, e->cfg.vocab);
