@@ -88,6 +88,19 @@ inline int launch(void (*kernel)(Params...), dim3 grid, dim3 block, size_t shmem
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---------------------------------------------------------------------------------------------
+// Block barrier for LDS traffic only. __syncthreads() is a workgroup fence over every address
+// space, for which the compiler waits for all of the wave's outstanding global loads and stores
+// (s_waitcnt vmcnt(0)) before s_barrier; this one waits for the wave's LDS accesses alone, so
+// global loads issued before it stay in flight across it. For barriers that order LDS accesses
+// only.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 }  // namespace llmk

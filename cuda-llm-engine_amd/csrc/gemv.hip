@@ -22,8 +22,12 @@
 //     VGPRs, 5 waves per SIMD, against 130 and 3). The waves' sums meet in LDS.
 //   - A normalising launch stages each wave's raw x slice in LDS once; the norms are taken from
 //     there instead of every wave re-reading whole rows.
+//   - Launches of 5 to 8 rows with at most kMfmaMaxOut outputs run the same blocks on the matrix
+//     cores instead (k_rows_mfma, v_mfma_f32_4x4x4_16b_f16; rows_launch_tp says why).
 // Summation order differs from cuBLAS/hipBLASLt (lane-strided partial sums, then the butterfly),
 // so results agree with the fp32 dot product to fp32 rounding, not bit for bit.
+#include <type_traits>
+
 #include "common.hpp"
 #include "pointwise.hpp"
 
@@ -166,6 +170,60 @@ __device__ __forceinline__ int row_of(int b, int r, const RowsArgs& a) {
   }
 }
 
+// The block's epilogue (see Epi): part[wave][r * TPP + t] holds each wave's sum for output row r
+// of the block (0..7) and token t (TPP >= T tokens computed); the waves' sums are added here.
+template <int EPI, int TPP, int WV>
+__device__ __forceinline__ void rows_epilogue(const RowsArgs& a, int b,
+                                              const float (&part)[WV][kRows * TPP]) {
+  const int T = a.T;
+  auto total = [&](int i) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < WV; ++q) sum += part[q][i];
+    return sum;
+  };
+  const int tid = threadIdx.x;
+  if constexpr (EPI == kEpiStore || EPI == kEpiResidual) {
+    if (tid < kRows * TPP) {
+      const int r = tid / TPP, t = tid % TPP, j = b * kRows + r;
+      if (j < a.out && t < T) {
+        const f16 p = (f16)total(tid);
+        f16* dst = a.y + (size_t)t * a.out + j;
+        *dst = EPI == kEpiStore ? p : (f16)((float)*dst + (float)p);
+      }
+    }
+  } else if (tid < 4 * TPP) {
+    const int r = tid / TPP, t = tid % TPP;  // the pair (r, r + 4) of token t
+    if (t < T) {
+      const f16 lo = (f16)total(tid), hi = (f16)total(tid + 4 * TPP);
+      if constexpr (EPI == kEpiSwiglu) {
+        const int inter = a.out / 2, j = 4 * b + r;
+        a.y[(size_t)t * inter + j] = silu_r16(lo) * hi;
+      } else {
+        const int h = b >> 3, i = 4 * (b & 7) + r, nq = a.n_heads, nkv = a.n_kv_heads;
+        const int pos = a.positions[t];
+        f16 x1 = lo, x2 = hi;
+        if (h < nq + nkv) {
+          f16 c, sn;
+          cos_sin_f16((float)pos * a.inv_freq[i], &c, &sn);
+          x1 = lo * c - hi * sn;
+          x2 = hi * c + lo * sn;
+        }
+        f16* dst;
+        if (h < nq) {
+          dst = a.q_out + ((size_t)t * nq + h) * 64;
+        } else {
+          const size_t prow = (size_t)a.tables[(size_t)t * a.max_pages + pos / 16] * 16 + pos % 16;
+          const int hk = h < nq + nkv ? h - nq : h - nq - nkv;
+          dst = (h < nq + nkv ? a.k_pool : a.v_pool) + prow * nkv * 64 + hk * 64;
+        }
+        dst[i] = x1;
+        dst[i + 32] = x2;
+      }
+    }
+  }
+}
+
 // TP: rows computed (a power of two >= T; rows t >= T reuse row T - 1 and are not stored).
 // WV: waves per block, dividing the in dimension's steps between them.
 // NORM: x is RMSNorm-ed on the fly; the launcher then gives every wave exactly one step
@@ -222,7 +280,7 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < TP; ++t) xs[t][wave][lane] = xv[t];
-    __syncthreads();
+    lds_barrier();  // the W loads stay in flight through the norms
     constexpr int NQ = (TP + WV - 1) / WV;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -242,7 +300,7 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
         if (lane == 0) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
       }
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int t = 0; t < TP; ++t) {
       const f16x8 h = as_h8(xv[t]);
@@ -275,52 +333,208 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
   const float* v = red;
   if (writer) part[wave][idx] = v[0];
   __syncthreads();
-  auto total = [&](int i) {
-    float sum = 0.0f;
+  rows_epilogue<EPI, TP, WV>(a, b, part);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The same products on the matrix cores: v_mfma_f32_4x4x4_16b_f16 computes 16 independent
+// 4 x 4 x 4 products; block q of the instruction is lanes 4q .. 4q + 3, lane 4q + i holding row i
+// of its A (4 k values, 64 bits), lane 4q + j column j of its B and D[0..3][j] (checked on
+// gfx950 with one-hot and index-coded operands). Here A is 4 tokens of x and B 4 rows of W, and
+// the 16 blocks take 16 different slices of k, so a wave's 16-byte load of W covers 4 rows x
+// 256 contiguous bytes (lane 4q + j: row j, k = 8q .. 8q + 7 of a 128-wide chunk) and four such
+// loads the rows' 1 KiB of a step, the bytes the dot-product kernel loads; each 16-byte load
+// feeds two instructions (k = 8q .. 8q + 3 and 8q + 4 .. 8q + 7). The block slices are summed
+// once, after the last step, by a four-exchange butterfly over lane bits 2-5.
+// ---------------------------------------------------------------------------------------------
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma4(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b),
+                                           c, 0, 0, 0);
+}
+__device__ __forceinline__ u32x2 lo2(u32x4 v) { return u32x2{v[0], v[1]}; }
+__device__ __forceinline__ u32x2 hi2(u32x4 v) { return u32x2{v[2], v[3]}; }
+
+// The value lane (lane ^ M) holds, M = 4, 8 (DPP inside a 16-lane row) or 16, 32 (swizzle).
+template <int M>
+__device__ __forceinline__ float xpartner(float v) {
+  if constexpr (M == 4 || M == 8) {
+    const int x = __builtin_bit_cast(int, v);
+    const int up = __builtin_amdgcn_mov_dpp(x, 0x110 + M, 0xF, 0xF, false);  // row_shr:M
+    const int dn = __builtin_amdgcn_mov_dpp(x, 0x100 + M, 0xF, 0xF, false);  // row_shl:M
+    return __builtin_bit_cast(float, (threadIdx.x & M) ? up : dn);
+  } else {
+    return __shfl_xor(v, M);
+  }
+}
+
+template <int TP, int WV, int EPI, bool NORM>
+__global__ void __launch_bounds__(64 * WV) k_rows_mfma(RowsArgs a) {
+  constexpr int TQ = TP <= 4 ? 1 : 2;  // token quads
+  constexpr int TPP = 4 * TQ;          // tokens computed (rows >= T repeat row T - 1, unstored)
+  constexpr int NV = 8 * TQ;           // values per lane: index (p * 2 + rq) * 4 + v
+  __shared__ float part[WV][kRows * TPP];
+  __shared__ float inv_s[TP];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = blockIdx.x;
+  const int in = a.in, T = a.T;
+  const int steps = in / kStep;
+  const int qb = lane >> 2, q4 = lane & 3;  // the lane's instruction block and its row in it
+
+  f32x4 acc[TQ][2];
 #pragma unroll
-    for (int q = 0; q < WV; ++q) sum += part[q][i];
-    return sum;
+  for (int p = 0; p < TQ; ++p)
+#pragma unroll
+    for (int rq = 0; rq < 2; ++rq) acc[p][rq] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f16* wr[2];
+#pragma unroll
+  for (int rq = 0; rq < 2; ++rq)
+    wr[rq] = a.w + (size_t)row_of<EPI>(b, 4 * rq + q4, a) * in + 8 * qb;
+  int tok[TQ];
+#pragma unroll
+  for (int p = 0; p < TQ; ++p) tok[p] = 4 * p + q4 < T ? 4 * p + q4 : T - 1;
+  auto chunk = [&](const u32x4 (&wv)[2], const u32x4 (&xv)[TQ]) {
+#pragma unroll
+    for (int p = 0; p < TQ; ++p)
+#pragma unroll
+      for (int rq = 0; rq < 2; ++rq) {
+        acc[p][rq] = mfma4(lo2(xv[p]), lo2(wv[rq]), acc[p][rq]);
+        acc[p][rq] = mfma4(hi2(xv[p]), hi2(wv[rq]), acc[p][rq]);
+      }
   };
-  const int tid = threadIdx.x;
-  if constexpr (EPI == kEpiStore || EPI == kEpiResidual) {
-    if (tid < N) {
-      const int r = tid / TP, t = tid % TP, j = b * kRows + r;
-      if (j < a.out && t < T) {
-        const f16 p = (f16)total(tid);
-        f16* dst = a.y + (size_t)t * a.out + j;
-        *dst = EPI == kEpiStore ? p : (f16)((float)*dst + (float)p);
+
+  if constexpr (NORM) {
+    // As in k_rows: every wave stages its step of the TP rows in LDS (the lane-strided layout
+    // of the RMSNorm kernel), wave t % WV takes row t's sum of squares in that kernel's order,
+    // and each lane then normalises the 16 bytes its instructions need, read back from LDS.
+    __shared__ u32x4 xs[TP][WV][64];
+    const size_t k0 = (size_t)wave * kStep;  // this wave's one step
+    // x first, then the norm weights, then W: the waits for the first two leave W in flight
+    // (memory waits are in issue order), and the barriers below order LDS accesses only.
+    u32x4 xl[TP], wv[4][2], nw[4];
+#pragma unroll
+    for (int t = 0; t < TP; ++t)
+      xl[t] = ld16(a.x + (size_t)(t < T ? t : T - 1) * in + k0 + lane * 8);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) nw[c] = ld16(a.norm_w + k0 + 128 * c + 8 * qb);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int rq = 0; rq < 2; ++rq) wv[c][rq] = ld16_stream(wr[rq] + k0 + 128 * c);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < TP; ++t) xs[t][wave][lane] = xl[t];
+    lds_barrier();
+    constexpr int NQ = (TP + WV - 1) / WV;
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq) {
+      const int t = wave + WV * qq;
+      if (t < TP) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < WV; ++k) {
+          const f16x8 h = as_h8(xs[t][k][lane]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float f = (float)h[j];
+            ss = ss + f * f;
+          }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
       }
     }
-  } else if (tid < 4 * TP) {
-    const int r = tid / TP, t = tid % TP;  // the pair (r, r + 4) of token t
-    if (t < T) {
-      const f16 lo = (f16)total(tid), hi = (f16)total(tid + 4 * TP);
-      if constexpr (EPI == kEpiSwiglu) {
-        const int inter = a.out / 2, j = 4 * b + r;
-        a.y[(size_t)t * inter + j] = silu_r16(lo) * hi;
+    lds_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 xv[TQ];
+#pragma unroll
+      for (int p = 0; p < TQ; ++p) {
+        const f16x8 h = as_h8(xs[tok[p]][wave][16 * c + qb]);
+        const float inv = inv_s[tok[p]];
+        f16x8 an;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
+        xv[p] = as_u4(as_h8(nw[c]) * an);
+      }
+      chunk(wv[c], xv);
+    }
+  } else {
+    const f16* xr[TQ];
+#pragma unroll
+    for (int p = 0; p < TQ; ++p) xr[p] = a.x + (size_t)tok[p] * in + 8 * qb;
+    for (int s = wave; s < steps; s += WV) {
+      const size_t k = (size_t)s * kStep;
+      u32x4 wv[4][2], xv[4][TQ];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int rq = 0; rq < 2; ++rq) wv[c][rq] = ld16_stream(wr[rq] + k + 128 * c);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int p = 0; p < TQ; ++p) xv[c][p] = ld16(xr[p] + k + 128 * c);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) chunk(wv[c], xv[c]);
+    }
+  }
+
+  // Sum the 16 instruction blocks' slices: value index (p * 2 + rq) * 4 + v (token 4p + v, row
+  // 4rq + q4); the halving exchanges run over lane bits 2, 3, 4, 5 (masks 4, 8, 16, 32).
+  float v[NV];
+#pragma unroll
+  for (int p = 0; p < TQ; ++p)
+#pragma unroll
+    for (int rq = 0; rq < 2; ++rq)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[(p * 2 + rq) * 4 + e] = acc[p][rq][e];
+  auto exchange = [&](auto mtag, int n) {
+    constexpr int M = decltype(mtag)::value;
+    const bool up = (threadIdx.x & M) != 0;
+    if (n > 1) {
+#pragma unroll
+      for (int i = 0; i < NV / 2; ++i) {
+        if (i < n / 2) {
+          const float send = up ? v[i] : v[i + n / 2];
+          const float keep = up ? v[i + n / 2] : v[i];
+          v[i] = keep + xpartner<M>(send);
+        }
+      }
+    } else {
+      v[0] = v[0] + xpartner<M>(v[0]);
+    }
+  };
+  exchange(std::integral_constant<int, 4>{}, NV);
+  exchange(std::integral_constant<int, 8>{}, NV / 2);
+  exchange(std::integral_constant<int, 16>{}, NV / 4);
+  exchange(std::integral_constant<int, 32>{}, NV / 8);
+  // The lane's value index: bits from the top = lane bits 2, 3, 4, 5 of the halving exchanges
+  // (NV = 16: all four halve; NV = 8: three halve, and only the lane with bit 5 clear writes).
+  int idx = 0;
+  bool writer = true;
+  {
+    int n = NV;
+#pragma unroll
+    for (int sb = 2; sb < 6; ++sb) {
+      const int bit = (lane >> sb) & 1;
+      if (n > 1) {
+        idx = 2 * idx + bit;
+        n /= 2;
       } else {
-        const int h = b >> 3, i = 4 * (b & 7) + r, nq = a.n_heads, nkv = a.n_kv_heads;
-        const int pos = a.positions[t];
-        f16 x1 = lo, x2 = hi;
-        if (h < nq + nkv) {
-          f16 c, sn;
-          cos_sin_f16((float)pos * a.inv_freq[i], &c, &sn);
-          x1 = lo * c - hi * sn;
-          x2 = hi * c + lo * sn;
-        }
-        f16* dst;
-        if (h < nq) {
-          dst = a.q_out + ((size_t)t * nq + h) * 64;
-        } else {
-          const size_t prow = (size_t)a.tables[(size_t)t * a.max_pages + pos / 16] * 16 + pos % 16;
-          const int hk = h < nq + nkv ? h - nq : h - nq - nkv;
-          dst = (h < nq + nkv ? a.k_pool : a.v_pool) + prow * nkv * 64 + hk * 64;
-        }
-        dst[i] = x1;
-        dst[i + 32] = x2;
+        writer = writer && bit == 0;
       }
     }
   }
+  const int pr = idx >> 2, e = idx & 3;  // (p * 2 + rq), v
+  const int t = 4 * (pr >> 1) + e, r = 4 * (pr & 1) + q4;
+  if (writer) part[wave][r * TPP + t] = v[0];
+  __syncthreads();
+  rows_epilogue<EPI, TPP, WV>(a, b, part);
 }
 
 // Waves per block: one per step of the in dimension, up to 16. A normalising launch needs
@@ -335,18 +549,36 @@ int rows_waves(int steps, bool norm) {
   return steps <= 1 ? 1 : steps <= 2 ? 2 : steps <= 4 ? 4 : steps <= 8 ? 8 : cap;
 }
 
+// Which kernel: the matrix-core kernel (k_rows_mfma) for 5 to 8 rows and at most
+// kMfmaMaxOut output features, the dot-product kernel (k_rows) otherwise. The rule looks only at
+// the row count and the output width, so a fused launch (RMSNorm + QKV + RoPE, RMSNorm + gate/up
+// + SwiGLU, a projection + residual) and the unfused launches it replaces run the same kernel
+// and give the same bits. Same box, Llama-3.2-1B shapes, weights rotated past the caches, us
+// (dot products -> matrix cores) at 8 rows: RMSNorm + gate/up + SwiGLU 19.1 -> 17.0, RMSNorm +
+// the QKV shape 7.34 -> 6.09, o + residual 6.32 -> 6.24, down + residual 9.25 -> 10.33, and the
+// lm head (128256 outputs) 93.1 -> 117.3, which therefore keeps the dot products; 4 rows of the
+// lm head 77.3 -> 86.1, 1 to 4 rows of the other shapes within 2% either way. (Each of the
+// matrix-core kernel's 16-byte loads covers 4 rows x 256 bytes rather than 1 KiB of one row.)
+constexpr int kMfmaMaxOut = 16384;
+
 template <int TP, int EPI, bool NORM>
 int rows_launch_tp(const RowsArgs& a, unsigned blocks, hipStream_t s) {
   const int wv = rows_waves<TP>(a.in / kStep, NORM);
+  const bool mfma = TP == 8 && a.out <= kMfmaMaxOut;
+#define LLMK_ROWS_LAUNCH(W)                                                                     \
+  if constexpr (TP == 8)                                                                        \
+    if (mfma)                                                                                   \
+      return launch(k_rows_mfma<TP, W, EPI, NORM>, dim3(blocks), dim3(64 * W), 0, s, a);      \
+  return launch(k_rows<TP, W, EPI, NORM>, dim3(blocks), dim3(64 * W), 0, s, a)
   switch (wv) {
-    case 1: return launch(k_rows<TP, 1, EPI, NORM>, dim3(blocks), dim3(64), 0, s, a);
-    case 2: return launch(k_rows<TP, 2, EPI, NORM>, dim3(blocks), dim3(128), 0, s, a);
-    case 4: return launch(k_rows<TP, 4, EPI, NORM>, dim3(blocks), dim3(256), 0, s, a);
-    case 8: return launch(k_rows<TP, 8, EPI, NORM>, dim3(blocks), dim3(512), 0, s, a);
-    case 16:
-      return launch(k_rows<TP, 16, EPI, NORM>, dim3(blocks), dim3(1024), 0, s, a);
+    case 1: LLMK_ROWS_LAUNCH(1);
+    case 2: LLMK_ROWS_LAUNCH(2);
+    case 4: LLMK_ROWS_LAUNCH(4);
+    case 8: LLMK_ROWS_LAUNCH(8);
+    case 16: LLMK_ROWS_LAUNCH(16);
     default: return LLMK_ERR_UNSUPPORTED;
   }
+#undef LLMK_ROWS_LAUNCH
 }
 
 template <int EPI, bool NORM>
