@@ -23,7 +23,11 @@
 //   - A normalising launch stages each wave's raw x slice in LDS once; the norms are taken from
 //     there instead of every wave re-reading whole rows.
 //   - Launches of 5 to 8 rows with at most kMfmaMaxOut outputs run the same blocks on the matrix
-//     cores instead (k_rows_mfma, v_mfma_f32_4x4x4_16b_f16; rows_launch_tp says why).
+//     cores instead (k_rows_mfma, v_mfma_f32_4x4x4_16b_f16; rows_launch_tp says why), and
+//     normalising ones with many output rows (gate/up) run 16-wave blocks that stage x once per
+//     64 rows through direct-to-LDS loads (k_rows_mfma_wide).
+//   - A residual epilogue reads the value it adds to at the start of the kernel, not after the
+//     products (0.25-0.3 us per launch on the o and down shapes at every row count).
 // Summation order differs from cuBLAS/hipBLASLt (lane-strided partial sums, then the butterfly),
 // so results agree with the fp32 dot product to fp32 rounding, not bit for bit.
 #include <type_traits>
@@ -170,11 +174,33 @@ __device__ __forceinline__ int row_of(int b, int r, const RowsArgs& a) {
   }
 }
 
-// The block's epilogue (see Epi): part[wave][r * TPP + t] holds each wave's sum for output row r
-// of the block (0..7) and token t (TPP >= T tokens computed); the waves' sums are added here.
+// Threads of the epilogue of one row group: one per (row, token) for a plain or residual store,
+// one per pair of rows (gate and up, or the two halves of a rotation) and token otherwise.
+template <int EPI, int TPP>
+constexpr int epi_threads() {
+  return EPI == kEpiStore || EPI == kEpiResidual ? kRows * TPP : 4 * TPP;
+}
+
+// kEpiResidual: the residual value epilogue thread `tid` of row group b adds to. Read at the start
+// of the kernel, so that this read is not a memory round trip after the products.
+template <int EPI, int TPP>
+__device__ __forceinline__ f16 epi_residual(const RowsArgs& a, int b, int tid) {
+  if constexpr (EPI == kEpiResidual) {
+    if (tid < kRows * TPP) {
+      const int r = tid / TPP, t = tid % TPP, j = b * kRows + r;
+      if (j < a.out && t < a.T) return a.y[(size_t)t * a.out + j];
+    }
+  }
+  return (f16)0.0f;
+}
+
+// The epilogue of row group b (see Epi), by threads tid < epi_threads: part[wave][r * TPP + t]
+// holds each wave's sum for output row r of the group (0..7) and token t (TPP >= T tokens
+// computed); the waves' sums are added here. res: epi_residual's value for this thread.
 template <int EPI, int TPP, int WV>
 __device__ __forceinline__ void rows_epilogue(const RowsArgs& a, int b,
-                                              const float (&part)[WV][kRows * TPP]) {
+                                              const float (&part)[WV][kRows * TPP], int tid,
+                                              f16 res) {
   const int T = a.T;
   auto total = [&](int i) {
     float sum = 0.0f;
@@ -182,14 +208,13 @@ __device__ __forceinline__ void rows_epilogue(const RowsArgs& a, int b,
     for (int q = 0; q < WV; ++q) sum += part[q][i];
     return sum;
   };
-  const int tid = threadIdx.x;
   if constexpr (EPI == kEpiStore || EPI == kEpiResidual) {
     if (tid < kRows * TPP) {
       const int r = tid / TPP, t = tid % TPP, j = b * kRows + r;
       if (j < a.out && t < T) {
         const f16 p = (f16)total(tid);
         f16* dst = a.y + (size_t)t * a.out + j;
-        *dst = EPI == kEpiStore ? p : (f16)((float)*dst + (float)p);
+        *dst = EPI == kEpiStore ? p : (f16)((float)res + (float)p);
       }
     }
   } else if (tid < 4 * TPP) {
@@ -240,6 +265,7 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
   const int b = blockIdx.x;
   const int in = a.in, T = a.T;
   const int steps = in / kStep;
+  const f16 res = epi_residual<EPI, TP>(a, b, threadIdx.x);
 
   // Token-major value index t * 8 + r: the butterfly's first log2(TP) halvings pair tokens of
   // one row, so they run row by row right after its dot products, and only the row's TP sums
@@ -333,7 +359,7 @@ __global__ void __launch_bounds__(64 * WV) k_rows(RowsArgs a) {
   const float* v = red;
   if (writer) part[wave][idx] = v[0];
   __syncthreads();
-  rows_epilogue<EPI, TP, WV>(a, b, part);
+  rows_epilogue<EPI, TP, WV>(a, b, part, threadIdx.x, res);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -371,11 +397,82 @@ __device__ __forceinline__ float xpartner(float v) {
   }
 }
 
+// The 16 bytes of x (token quad p: tokens 4p .. 4p + 3) and of two W row quads (rq: rows 4rq ..
+// 4rq + 3) at one k slice of the lane: two instructions per row quad, k = 8q .. 8q + 3 and
+// 8q + 4 .. 8q + 7.
+template <int TQ>
+__device__ __forceinline__ void mfma_chunk(f32x4 (&acc)[TQ][2], const u32x4 (&wv)[2],
+                                           const u32x4 (&xv)[TQ]) {
+#pragma unroll
+  for (int p = 0; p < TQ; ++p)
+#pragma unroll
+    for (int rq = 0; rq < 2; ++rq) {
+      acc[p][rq] = mfma4(lo2(xv[p]), lo2(wv[rq]), acc[p][rq]);
+      acc[p][rq] = mfma4(hi2(xv[p]), hi2(wv[rq]), acc[p][rq]);
+    }
+}
+
+// Sums the 16 instruction blocks' slices of a wave's accumulators and stores the wave's sum of
+// each (row, token) of its row group into part[r * TPP + t]: value index (p * 2 + rq) * 4 + v
+// (token 4p + v, row 4rq + q4), halved over lane bits 2, 3, 4, 5 (masks 4, 8, 16, 32).
+template <int TQ>
+__device__ __forceinline__ void mfma_store_part(const f32x4 (&acc)[TQ][2], float* part) {
+  constexpr int TPP = 4 * TQ;
+  constexpr int NV = 8 * TQ;  // values per lane
+  const int lane = threadIdx.x & 63;
+  float v[NV];
+#pragma unroll
+  for (int p = 0; p < TQ; ++p)
+#pragma unroll
+    for (int rq = 0; rq < 2; ++rq)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[(p * 2 + rq) * 4 + e] = acc[p][rq][e];
+  auto exchange = [&](auto mtag, int n) {
+    constexpr int M = decltype(mtag)::value;
+    const bool up = (threadIdx.x & M) != 0;
+    if (n > 1) {
+#pragma unroll
+      for (int i = 0; i < NV / 2; ++i) {
+        if (i < n / 2) {
+          const float send = up ? v[i] : v[i + n / 2];
+          const float keep = up ? v[i + n / 2] : v[i];
+          v[i] = keep + xpartner<M>(send);
+        }
+      }
+    } else {
+      v[0] = v[0] + xpartner<M>(v[0]);
+    }
+  };
+  exchange(std::integral_constant<int, 4>{}, NV);
+  exchange(std::integral_constant<int, 8>{}, NV / 2);
+  exchange(std::integral_constant<int, 16>{}, NV / 4);
+  exchange(std::integral_constant<int, 32>{}, NV / 8);
+  // The lane's value index: bits from the top = lane bits 2, 3, 4, 5 of the halving exchanges
+  // (NV = 16: all four halve; NV = 8: three halve, and only the lane with bit 5 clear writes).
+  int idx = 0;
+  bool writer = true;
+  {
+    int n = NV;
+#pragma unroll
+    for (int sb = 2; sb < 6; ++sb) {
+      const int bit = (lane >> sb) & 1;
+      if (n > 1) {
+        idx = 2 * idx + bit;
+        n /= 2;
+      } else {
+        writer = writer && bit == 0;
+      }
+    }
+  }
+  const int pr = idx >> 2, e = idx & 3;  // (p * 2 + rq), v
+  const int t = 4 * (pr >> 1) + e, r = 4 * (pr & 1) + (lane & 3);
+  if (writer) part[r * TPP + t] = v[0];
+}
+
 template <int TP, int WV, int EPI, bool NORM>
 __global__ void __launch_bounds__(64 * WV) k_rows_mfma(RowsArgs a) {
   constexpr int TQ = TP <= 4 ? 1 : 2;  // token quads
   constexpr int TPP = 4 * TQ;          // tokens computed (rows >= T repeat row T - 1, unstored)
-  constexpr int NV = 8 * TQ;           // values per lane: index (p * 2 + rq) * 4 + v
   __shared__ float part[WV][kRows * TPP];
   __shared__ float inv_s[TP];
   const int lane = threadIdx.x & 63;
@@ -384,6 +481,7 @@ __global__ void __launch_bounds__(64 * WV) k_rows_mfma(RowsArgs a) {
   const int in = a.in, T = a.T;
   const int steps = in / kStep;
   const int qb = lane >> 2, q4 = lane & 3;  // the lane's instruction block and its row in it
+  const f16 res = epi_residual<EPI, TPP>(a, b, threadIdx.x);
 
   f32x4 acc[TQ][2];
 #pragma unroll
@@ -397,15 +495,6 @@ __global__ void __launch_bounds__(64 * WV) k_rows_mfma(RowsArgs a) {
   int tok[TQ];
 #pragma unroll
   for (int p = 0; p < TQ; ++p) tok[p] = 4 * p + q4 < T ? 4 * p + q4 : T - 1;
-  auto chunk = [&](const u32x4 (&wv)[2], const u32x4 (&xv)[TQ]) {
-#pragma unroll
-    for (int p = 0; p < TQ; ++p)
-#pragma unroll
-      for (int rq = 0; rq < 2; ++rq) {
-        acc[p][rq] = mfma4(lo2(xv[p]), lo2(wv[rq]), acc[p][rq]);
-        acc[p][rq] = mfma4(hi2(xv[p]), hi2(wv[rq]), acc[p][rq]);
-      }
-  };
 
   if constexpr (NORM) {
     // As in k_rows: every wave stages its step of the TP rows in LDS (the lane-strided layout
@@ -461,7 +550,7 @@ __global__ void __launch_bounds__(64 * WV) k_rows_mfma(RowsArgs a) {
         for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
         xv[p] = as_u4(as_h8(nw[c]) * an);
       }
-      chunk(wv[c], xv);
+      mfma_chunk<TQ>(acc, wv[c], xv);
     }
   } else {
     const f16* xr[TQ];
@@ -480,61 +569,144 @@ __global__ void __launch_bounds__(64 * WV) k_rows_mfma(RowsArgs a) {
         for (int p = 0; p < TQ; ++p) xv[c][p] = ld16(xr[p] + k + 128 * c);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) chunk(wv[c], xv[c]);
+      for (int c = 0; c < 4; ++c) mfma_chunk<TQ>(acc, wv[c], xv[c]);
     }
   }
 
-  // Sum the 16 instruction blocks' slices: value index (p * 2 + rq) * 4 + v (token 4p + v, row
-  // 4rq + q4); the halving exchanges run over lane bits 2, 3, 4, 5 (masks 4, 8, 16, 32).
-  float v[NV];
-#pragma unroll
-  for (int p = 0; p < TQ; ++p)
-#pragma unroll
-    for (int rq = 0; rq < 2; ++rq)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[(p * 2 + rq) * 4 + e] = acc[p][rq][e];
-  auto exchange = [&](auto mtag, int n) {
-    constexpr int M = decltype(mtag)::value;
-    const bool up = (threadIdx.x & M) != 0;
-    if (n > 1) {
-#pragma unroll
-      for (int i = 0; i < NV / 2; ++i) {
-        if (i < n / 2) {
-          const float send = up ? v[i] : v[i + n / 2];
-          const float keep = up ? v[i + n / 2] : v[i];
-          v[i] = keep + xpartner<M>(send);
-        }
-      }
-    } else {
-      v[0] = v[0] + xpartner<M>(v[0]);
-    }
-  };
-  exchange(std::integral_constant<int, 4>{}, NV);
-  exchange(std::integral_constant<int, 8>{}, NV / 2);
-  exchange(std::integral_constant<int, 16>{}, NV / 4);
-  exchange(std::integral_constant<int, 32>{}, NV / 8);
-  // The lane's value index: bits from the top = lane bits 2, 3, 4, 5 of the halving exchanges
-  // (NV = 16: all four halve; NV = 8: three halve, and only the lane with bit 5 clear writes).
-  int idx = 0;
-  bool writer = true;
-  {
-    int n = NV;
-#pragma unroll
-    for (int sb = 2; sb < 6; ++sb) {
-      const int bit = (lane >> sb) & 1;
-      if (n > 1) {
-        idx = 2 * idx + bit;
-        n /= 2;
-      } else {
-        writer = writer && bit == 0;
-      }
-    }
-  }
-  const int pr = idx >> 2, e = idx & 3;  // (p * 2 + rq), v
-  const int t = 4 * (pr >> 1) + e, r = 4 * (pr & 1) + q4;
-  if (writer) part[wave][r * TPP + t] = v[0];
+  mfma_store_part<TQ>(acc, part[wave]);
   __syncthreads();
-  rows_epilogue<EPI, TPP, WV>(a, b, part);
+  rows_epilogue<EPI, TPP, WV>(a, b, part, threadIdx.x, res);
+}
+
+// ---------------------------------------------------------------------------------------------
+// 5 to 8 rows, RMSNorm prologue, many output rows (the gate/up projection): blocks of 16 waves,
+// WV steps of the in dimension x RG row-group pairs, so that x is staged and normalised once per
+// 16 * RG output rows rather than once per 8.
+//   - The block's x rows and the norm weights go from memory straight into LDS
+//     (global_load_lds_dwordx4: no registers held while they are in flight).
+//   - Each wave streams 16 W rows (two row groups) of its step into registers: 16 KiB in flight
+//     per wave, 256 KiB per CU with one block per CU, the one-row kernel's figure.
+//   - Row t's sum of squares is taken by wave t in the RMSNorm kernel's order, the block's x is
+//     normalised in place in LDS once, and the products, the waves' sums and the epilogues are
+//     those of k_rows_mfma: every output has k_rows_mfma's bits.
+// The compiler cannot tell which outstanding loads an LDS read after global_load_lds depends on
+// and waits for all of them (s_waitcnt vmcnt(0)) at an LDS fence, which would hold the barriers
+// until every W load had landed. So each wave waits for exactly its own DMA loads (issued before
+// its W loads; loads complete in issue order) and for its own LDS writes, and then crosses a plain
+// s_barrier (dma_barrier).
+// ---------------------------------------------------------------------------------------------
+template <int VM, int LGKM>
+__device__ __forceinline__ void wait_vm_lgkm() {  // s_waitcnt vmcnt(VM) lgkmcnt(LGKM), gfx9 fields
+  static_assert(VM >= 0 && VM < 64 && LGKM >= 0 && LGKM < 16, "waitcnt field range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (LGKM << 8));
+}
+__device__ __forceinline__ void dma_barrier() {
+  asm volatile("" ::: "memory");  // no LDS access moves across the barrier
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+typedef __attribute__((address_space(3))) void lds_void;
+// 16 bytes per lane from `g` into LDS at `wave_base` + 16 * lane (wave_base is the wave's).
+__device__ __forceinline__ void dma16(const void* g, void* wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)wave_base, 16, 0, 0);
+}
+
+template <int WV, int RG, int EPI>
+__global__ void __launch_bounds__(64 * WV * RG, 1) k_rows_mfma_wide(RowsArgs a) {
+  constexpr int TP = 8, TQ = 2, TPP = 8, G = 2;  // G: row groups per wave
+  constexpr int NW = WV * RG;                     // waves per block
+  constexpr int NWL = 4 * G * 2;                  // W loads per wave
+  static_assert(NW <= 16 && NW >= TP, "one wave per row's sum of squares");
+  static_assert(EPI != kEpiResidual, "the residual epilogue has no RMSNorm prologue");
+  __shared__ float part[RG * G][WV][kRows * TPP];
+  __shared__ float inv_s[TP];
+  __shared__ u32x4 xs[TP][WV][64];
+  __shared__ u32x4 nws[WV][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int step = wave % WV, rg = wave / WV;
+  const int in = a.in, T = a.T;
+  const int qb = lane >> 2, q4 = lane & 3;
+  const int g0 = (blockIdx.x * RG + rg) * G;  // the wave's first row group
+
+  f32x4 acc[G][TQ][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int p = 0; p < TQ; ++p)
+#pragma unroll
+      for (int rq = 0; rq < 2; ++rq) acc[g][p][rq] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int tok[TQ];
+#pragma unroll
+  for (int p = 0; p < TQ; ++p) tok[p] = 4 * p + q4 < T ? 4 * p + q4 : T - 1;
+
+  // The (row, step) slices of x and the steps of the norm weights, spread over the waves.
+  for (int i = wave; i < (TP + 1) * WV; i += NW) {
+    const int t = i / WV, k = i % WV;
+    if (t < TP)
+      dma16(a.x + (size_t)(t < T ? t : T - 1) * in + (size_t)k * kStep + lane * 8, &xs[t][k][0]);
+    else
+      dma16(a.norm_w + (size_t)k * kStep + lane * 8, &nws[k][0]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const size_t k0 = (size_t)step * kStep;
+  u32x4 wv[4][G][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int rq = 0; rq < 2; ++rq)
+        wv[c][g][rq] = ld16_stream(a.w + (size_t)row_of<EPI>(g0 + g, 4 * rq + q4, a) * in +
+                                   k0 + 128 * c + 8 * qb);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm_lgkm<NWL, 15>();  // this wave's DMA loads have landed; its W loads stay in flight
+  dma_barrier();
+  if (wave < TP) {
+    const int t = wave;
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < WV; ++k) {
+      const f16x8 h = as_h8(xs[t][k][lane]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float f = (float)h[j];
+        ss = ss + f * f;
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
+  }
+  wait_vm_lgkm<63, 0>();
+  dma_barrier();
+  for (int i = wave; i < TP * WV; i += NW) {
+    const int t = i / WV, k = i % WV;
+    const f16x8 h = as_h8(xs[t][k][lane]);
+    const float inv = inv_s[t];
+    f16x8 an;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
+    xs[t][k][lane] = as_u4(as_h8(nws[k][lane]) * an);
+  }
+  wait_vm_lgkm<63, 0>();
+  dma_barrier();
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    u32x4 xv[TQ];
+#pragma unroll
+    for (int p = 0; p < TQ; ++p) xv[p] = xs[tok[p]][step][16 * c + qb];
+#pragma unroll
+    for (int g = 0; g < G; ++g) mfma_chunk<TQ>(acc[g], wv[c][g], xv);
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) mfma_store_part<TQ>(acc[g], part[rg * G + g][step]);
+  __syncthreads();
+  // The RG * G row groups' epilogues, side by side.
+  constexpr int E = epi_threads<EPI, TPP>();
+  static_assert(RG * G * E <= 64 * NW, "threads for every epilogue");
+  const int e = threadIdx.x / E, tid = threadIdx.x % E;
+  if (e < RG * G)
+    rows_epilogue<EPI, TPP, WV>(a, blockIdx.x * RG * G + e, part[e], tid, (f16)0.0f);
 }
 
 // Waves per block: one per step of the in dimension, up to 16. A normalising launch needs
@@ -549,11 +721,11 @@ int rows_waves(int steps, bool norm) {
   return steps <= 1 ? 1 : steps <= 2 ? 2 : steps <= 4 ? 4 : steps <= 8 ? 8 : cap;
 }
 
-// Which kernel: the matrix-core kernel (k_rows_mfma) for 5 to 8 rows and at most
-// kMfmaMaxOut output features, the dot-product kernel (k_rows) otherwise. The rule looks only at
-// the row count and the output width, so a fused launch (RMSNorm + QKV + RoPE, RMSNorm + gate/up
-// + SwiGLU, a projection + residual) and the unfused launches it replaces run the same kernel
-// and give the same bits. Same box, Llama-3.2-1B shapes, weights rotated past the caches, us
+// Which kernel: the matrix-core kernels (k_rows_mfma, k_rows_mfma_wide) for 5 to 8 rows and at
+// most kMfmaMaxOut output features, the dot-product kernel (k_rows) otherwise. The family is
+// chosen by the row count and the output width alone, and both matrix-core kernels sum every
+// output in the same order, so a fused launch (RMSNorm + QKV + RoPE, RMSNorm + gate/up + SwiGLU,
+// a projection + residual) and the unfused launches it replaces give the same bits. Same box, Llama-3.2-1B shapes, weights rotated past the caches, us
 // (dot products -> matrix cores) at 8 rows: RMSNorm + gate/up + SwiGLU 19.1 -> 17.0, RMSNorm +
 // the QKV shape 7.34 -> 6.09, o + residual 6.32 -> 6.24, down + residual 9.25 -> 10.33, and the
 // lm head (128256 outputs) 93.1 -> 117.3, which therefore keeps the dot products; 4 rows of the
@@ -561,10 +733,30 @@ int rows_waves(int steps, bool norm) {
 // matrix-core kernel's 16-byte loads covers 4 rows x 256 bytes rather than 1 KiB of one row.)
 constexpr int kMfmaMaxOut = 16384;
 
+// k_rows_mfma_wide: normalising launches of that family with in = 2048 (4 steps, 4 row-group
+// pairs per block) and at least kWideMinGroups row groups, so that every CU gets a block
+// (gate/up of Llama-3.2-1B: 2048 groups, 256 blocks). Its outputs are k_rows_mfma's bits. Same
+// box, 8 rows, RMSNorm + gate/up + SwiGLU: 16.7-17.1 -> 14.8-14.9 us (5 rows 16.2 -> 14.6).
+constexpr int kWideWaves = 4, kWideRG = 4;
+constexpr unsigned kWideMinGroups = 2048;
+
+template <int EPI>
+int rows_launch_wide(const RowsArgs& a, unsigned blocks, hipStream_t s) {
+  if constexpr (EPI == kEpiResidual) {
+    return LLMK_ERR_UNSUPPORTED;
+  } else {
+    return launch(k_rows_mfma_wide<kWideWaves, kWideRG, EPI>, dim3(blocks / (2 * kWideRG)),
+                  dim3(64 * kWideWaves * kWideRG), 0, s, a);
+  }
+}
+
 template <int TP, int EPI, bool NORM>
 int rows_launch_tp(const RowsArgs& a, unsigned blocks, hipStream_t s) {
   const int wv = rows_waves<TP>(a.in / kStep, NORM);
   const bool mfma = TP == 8 && a.out <= kMfmaMaxOut;
+  if constexpr (TP == 8 && NORM && EPI != kEpiResidual)
+    if (mfma && wv == kWideWaves && blocks >= kWideMinGroups && blocks % (2 * kWideRG) == 0)
+      return rows_launch_wide<EPI>(a, blocks, s);
 #define LLMK_ROWS_LAUNCH(W)                                                                     \
   if constexpr (TP == 8)                                                                        \
     if (mfma)                                                                                   \

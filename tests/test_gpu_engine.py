@@ -200,6 +200,65 @@ def test_linear_rows_fused_give_the_bits_of_the_separate_launches(llmk, orc, T):
     assert int((host(pools[0]) != POISON).sum()) == T * kvdim  # one row per token, no more
 
 
+@pytest.mark.parametrize("T", [3, 5, 8])
+def test_linear_rows_wide_normalising_launches_give_the_bits_of_the_separate_launches(llmk, orc,
+                                                                                       T):
+    """Normalising few-rows launches with at least 2048 groups of 8 output rows (gate/up at
+    in = 2048; at 5 to 8 rows the 16-wave blocks that stage x in LDS once per 64 rows) against
+    RMSNorm + the plain few-rows projection + the separate epilogue: every output bit, for the
+    plain store, the SwiGLU epilogue and the RoPE / K/V scatter epilogue (240 query heads, so
+    that the QKV rows reach 2048 groups). T = 3 takes the dot-product kernel for both."""
+    rng = np.random.default_rng(0x5EED0250 + T)
+    H, eps, inter = 2048, 1e-5, 8192
+    x = dev(normal_f16(rng, (T, H)))
+    nw = dev(normal_f16(rng, (H,), 1.0, 0.1))
+    normed = torch.empty(T * H, dtype=torch.float16, device=DEV)
+    llmk.rmsnorm(x, nw, normed, T, H, eps)
+    wgu = dev(normal_f16(rng, (2 * inter, H), std=0.02))
+    print(f"wide few-rows T={T}: store", flush=True)
+    y1 = torch.full((T * 2 * inter,), float("nan"), dtype=torch.float16, device=DEV)
+    y2 = y1.clone()
+    llmk.linear_rows_norm(x, nw, eps, wgu, y1, T, H, 2 * inter)
+    llmk.linear_rows(normed, wgu, y2, T, H, 2 * inter)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(y1), host(y2))
+    bad, exact = linear_rule(host(y2), orc.linear(host(normed), host(wgu), T, H, 2 * inter,
+                                                  threads=16).ravel())
+    assert bad == 0 and exact > 0.9
+
+    print(f"wide few-rows T={T}: swiglu", flush=True)
+    act1 = torch.full((T * inter,), float("nan"), dtype=torch.float16, device=DEV)
+    act2 = act1.clone()
+    llmk.linear_rows_swiglu(x, nw, eps, wgu, act1, T, H, inter)
+    llmk.swiglu_rows(y2, act2, T, inter)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(act1), host(act2))
+
+    print(f"wide few-rows T={T}: qkv rope scatter", flush=True)
+    nh, nkv, hd, ps, max_pages = 240, 8, 64, 16, 4
+    qkvdim, kvdim = (nh + 2 * nkv) * hd, nkv * hd
+    num_pages = T * max_pages
+    wqkv = dev(normal_f16(rng, (qkvdim, H), std=0.05))
+    pos = dev_i32(rng.integers(0, max_pages * ps, T))
+    tables = dev_i32(rng.permutation(num_pages).reshape(T, max_pages))
+    inv = torch.from_numpy(orc.compute_rope_inv_freq(hd, 500000.0, 32.0, 1.0, 4.0,
+                                                     8192.0)).to(DEV)
+    pools = [dev(np.full(num_pages * ps * kvdim, POISON, np.uint16)) for _ in range(4)]
+    q1 = torch.full((T * nh * hd,), float("nan"), dtype=torch.float16, device=DEV)
+    q2 = q1.clone()
+    llmk.linear_rows_qkv_rope_scatter(x, nw, eps, wqkv, q1, pools[0], pools[1], tables, pos, inv,
+                                      T, H, nh, nkv, max_pages)
+    qkv = torch.empty(T * qkvdim, dtype=torch.float16, device=DEV)
+    llmk.linear_rows(normed, wqkv, qkv, T, H, qkvdim)
+    llmk.qkv_rope_scatter(qkv, qkvdim, q2, pools[2], pools[3], tables, pos, inv, T, max_pages,
+                          ps, nh, nkv, hd)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q1), host(q2))
+    assert np.array_equal(host(pools[0]), host(pools[2]))
+    assert np.array_equal(host(pools[1]), host(pools[3]))
+    assert int((host(pools[0]) != POISON).sum()) == T * kvdim
+
+
 def test_linear_rows_fused_preconditions(llmk):
     z = torch.zeros(8 * 8192 + 64, dtype=torch.float16, device=DEV)
     w = torch.zeros(64 * 8192, dtype=torch.float16, device=DEV)
