@@ -22,8 +22,9 @@
 //     VGPRs, 5 waves per SIMD, against 130 and 3). The waves' sums meet in LDS.
 //   - A normalising launch stages each wave's raw x slice in LDS once; the norms are taken from
 //     there instead of every wave re-reading whole rows.
-//   - Launches of 5 to 8 rows with at most kMfmaMaxOut outputs run the same blocks on the matrix
-//     cores instead (k_rows_mfma, v_mfma_f32_4x4x4_16b_f16; rows_launch_tp says why), and
+//   - Launches of 5 to 8 rows of matrices of at most kMfmaMaxOut x kMfmaMaxIn run the same
+//     blocks on the matrix cores instead (k_rows_mfma, v_mfma_f32_4x4x4_16b_f16;
+//     rows_launch_tp says why), and
 //     normalising ones with many output rows (gate/up) run 16-wave blocks that stage x once per
 //     64 rows through direct-to-LDS loads (k_rows_mfma_wide).
 //   - A residual epilogue reads the value it adds to at the start of the kernel, not after the
@@ -579,16 +580,16 @@ __global__ void __launch_bounds__(64 * WV) k_rows_mfma(RowsArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// 5 to 8 rows, RMSNorm prologue, many output rows (the gate/up projection): blocks of 16 waves,
-// WV steps of the in dimension x RG row-group pairs, so that x is staged and normalised once per
-// 16 * RG output rows rather than once per 8.
-//   - The block's x rows and the norm weights go from memory straight into LDS
+// 5 to 8 rows, many output rows (gate/up, the lm head): blocks of 16 waves, WV steps of the in
+// dimension x RG row-group pairs, so that x is staged (and normalised, NORM) once per 16 * RG
+// output rows rather than once per 8.
+//   - The block's x rows (and the norm weights) go from memory straight into LDS
 //     (global_load_lds_dwordx4: no registers held while they are in flight).
 //   - Each wave streams 16 W rows (two row groups) of its step into registers: 16 KiB in flight
 //     per wave, 256 KiB per CU with one block per CU, the one-row kernel's figure.
-//   - Row t's sum of squares is taken by wave t in the RMSNorm kernel's order, the block's x is
-//     normalised in place in LDS once, and the products, the waves' sums and the epilogues are
-//     those of k_rows_mfma: every output has k_rows_mfma's bits.
+//   - NORM: row t's sum of squares is taken by wave t in the RMSNorm kernel's order and the
+//     block's x is normalised in place in LDS once. The products, the waves' sums and the
+//     epilogues are those of k_rows_mfma: every output has k_rows_mfma's bits.
 // The compiler cannot tell which outstanding loads an LDS read after global_load_lds depends on
 // and waits for all of them (s_waitcnt vmcnt(0)) at an LDS fence, which would hold the barriers
 // until every W load had landed. So each wave waits for exactly its own DMA loads (issued before
@@ -611,13 +612,13 @@ __device__ __forceinline__ void dma16(const void* g, void* wave_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)wave_base, 16, 0, 0);
 }
 
-template <int WV, int RG, int EPI>
+template <int WV, int RG, int EPI, bool NORM>
 __global__ void __launch_bounds__(64 * WV * RG, 1) k_rows_mfma_wide(RowsArgs a) {
   constexpr int TP = 8, TQ = 2, TPP = 8, G = 2;  // G: row groups per wave
   constexpr int NW = WV * RG;                     // waves per block
   constexpr int NWL = 4 * G * 2;                  // W loads per wave
   static_assert(NW <= 16 && NW >= TP, "one wave per row's sum of squares");
-  static_assert(EPI != kEpiResidual, "the residual epilogue has no RMSNorm prologue");
+  static_assert(EPI != kEpiResidual, "the residual epilogue keeps the narrow kernels");
   __shared__ float part[RG * G][WV][kRows * TPP];
   __shared__ float inv_s[TP];
   __shared__ u32x4 xs[TP][WV][64];
@@ -641,7 +642,7 @@ __global__ void __launch_bounds__(64 * WV * RG, 1) k_rows_mfma_wide(RowsArgs a) 
   for (int p = 0; p < TQ; ++p) tok[p] = 4 * p + q4 < T ? 4 * p + q4 : T - 1;
 
   // The (row, step) slices of x and the steps of the norm weights, spread over the waves.
-  for (int i = wave; i < (TP + 1) * WV; i += NW) {
+  for (int i = wave; i < (NORM ? TP + 1 : TP) * WV; i += NW) {
     const int t = i / WV, k = i % WV;
     if (t < TP)
       dma16(a.x + (size_t)(t < T ? t : T - 1) * in + (size_t)k * kStep + lane * 8, &xs[t][k][0]);
@@ -662,34 +663,36 @@ __global__ void __launch_bounds__(64 * WV * RG, 1) k_rows_mfma_wide(RowsArgs a) 
   __builtin_amdgcn_sched_barrier(0);
   wait_vm_lgkm<NWL, 15>();  // this wave's DMA loads have landed; its W loads stay in flight
   dma_barrier();
-  if (wave < TP) {
-    const int t = wave;
-    float ss = 0.0f;
+  if constexpr (NORM) {
+    if (wave < TP) {
+      const int t = wave;
+      float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < WV; ++k) {
-      const f16x8 h = as_h8(xs[t][k][lane]);
+      for (int k = 0; k < WV; ++k) {
+        const f16x8 h = as_h8(xs[t][k][lane]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float f = (float)h[j];
-        ss = ss + f * f;
+        for (int j = 0; j < 8; ++j) {
+          const float f = (float)h[j];
+          ss = ss + f * f;
+        }
       }
+      ss = wave_sum(ss);
+      if (lane == 0) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
     }
-    ss = wave_sum(ss);
-    if (lane == 0) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
-  }
-  wait_vm_lgkm<63, 0>();
-  dma_barrier();
-  for (int i = wave; i < TP * WV; i += NW) {
-    const int t = i / WV, k = i % WV;
-    const f16x8 h = as_h8(xs[t][k][lane]);
-    const float inv = inv_s[t];
-    f16x8 an;
+    wait_vm_lgkm<63, 0>();
+    dma_barrier();
+    for (int i = wave; i < TP * WV; i += NW) {
+      const int t = i / WV, k = i % WV;
+      const f16x8 h = as_h8(xs[t][k][lane]);
+      const float inv = inv_s[t];
+      f16x8 an;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
-    xs[t][k][lane] = as_u4(as_h8(nws[k][lane]) * an);
+      for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
+      xs[t][k][lane] = as_u4(as_h8(nws[k][lane]) * an);
+    }
+    wait_vm_lgkm<63, 0>();
+    dma_barrier();
   }
-  wait_vm_lgkm<63, 0>();
-  dma_barrier();
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     u32x4 xv[TQ];
@@ -721,42 +724,50 @@ int rows_waves(int steps, bool norm) {
   return steps <= 1 ? 1 : steps <= 2 ? 2 : steps <= 4 ? 4 : steps <= 8 ? 8 : cap;
 }
 
-// Which kernel: the matrix-core kernels (k_rows_mfma, k_rows_mfma_wide) for 5 to 8 rows and at
-// most kMfmaMaxOut output features, the dot-product kernel (k_rows) otherwise. The family is
-// chosen by the row count and the output width alone, and both matrix-core kernels sum every
-// output in the same order, so a fused launch (RMSNorm + QKV + RoPE, RMSNorm + gate/up + SwiGLU,
-// a projection + residual) and the unfused launches it replaces give the same bits. Same box, Llama-3.2-1B shapes, weights rotated past the caches, us
-// (dot products -> matrix cores) at 8 rows: RMSNorm + gate/up + SwiGLU 19.1 -> 17.0, RMSNorm +
-// the QKV shape 7.34 -> 6.09, o + residual 6.32 -> 6.24, down + residual 9.25 -> 10.33, and the
-// lm head (128256 outputs) 93.1 -> 117.3, which therefore keeps the dot products; 4 rows of the
-// lm head 77.3 -> 86.1, 1 to 4 rows of the other shapes within 2% either way. (Each of the
-// matrix-core kernel's 16-byte loads covers 4 rows x 256 bytes rather than 1 KiB of one row.)
+// Which kernel: for 5 to 8 rows of a matrix with at most kMfmaMaxIn input features, the
+// matrix-core kernels (k_rows_mfma, k_rows_mfma_wide) up to kMfmaMaxOut output features and where
+// the wide kernel applies; the dot-product kernel (k_rows) otherwise. The family is chosen by the
+// row count and the matrix shape alone, and both matrix-core kernels sum every output in the
+// same order, so a fused launch (RMSNorm + QKV + RoPE, RMSNorm + gate/up + SwiGLU, a projection
+// + residual) and the unfused launches it replaces give the same bits. Same box, Llama-3.2-1B
+// shapes, weights rotated past the caches, us (dot products -> k_rows_mfma) at 8 rows: RMSNorm +
+// gate/up + SwiGLU 19.1 -> 17.0, RMSNorm + the QKV shape 7.34 -> 6.09, o + residual 6.32 ->
+// 6.24, and the lm head (128256 outputs) 93.1 -> 117.3, which therefore takes the wide kernel or
+// none; 4 rows of the lm head 77.3 -> 86.1, 1 to 4 rows of the other shapes within 2% either
+// way. (Each of the matrix-core kernels' 16-byte loads covers 4 rows x 256 bytes rather than
+// 1 KiB of one row.) Over in = 8192 (down + residual) the dot products win once the residual is
+// read at the start: 10.3 -> 9.0-9.3 us at 8 rows, equal at 5.
 constexpr int kMfmaMaxOut = 16384;
+constexpr int kMfmaMaxIn = 4096;
 
-// k_rows_mfma_wide: normalising launches of that family with in = 2048 (4 steps, 4 row-group
-// pairs per block) and at least kWideMinGroups row groups, so that every CU gets a block
-// (gate/up of Llama-3.2-1B: 2048 groups, 256 blocks). Its outputs are k_rows_mfma's bits. Same
-// box, 8 rows, RMSNorm + gate/up + SwiGLU: 16.7-17.1 -> 14.8-14.9 us (5 rows 16.2 -> 14.6).
+// k_rows_mfma_wide: launches of 5 to 8 rows with in = 2048 (4 steps, 4 row-group pairs per
+// block) and at least kWideMinGroups row groups, so that every CU gets a block (gate/up of
+// Llama-3.2-1B: 2048 groups, 256 blocks), except the residual epilogue; above kMfmaMaxOut
+// outputs too (the lm head), since there it beats the dot products as well. Its outputs are
+// k_rows_mfma's bits. Same box, 8 rows, us: RMSNorm + gate/up + SwiGLU 16.7-17.1 -> 14.8-14.9
+// (5 rows 16.2 -> 14.6), gate/up alone 17.1 -> 13.7, lm head (128256 x 2048) 93.7 -> 89.7,
+// with the RMSNorm 126 -> 96 (5 rows: equal, 88.5).
 constexpr int kWideWaves = 4, kWideRG = 4;
 constexpr unsigned kWideMinGroups = 2048;
 
-template <int EPI>
+template <int EPI, bool NORM>
 int rows_launch_wide(const RowsArgs& a, unsigned blocks, hipStream_t s) {
   if constexpr (EPI == kEpiResidual) {
     return LLMK_ERR_UNSUPPORTED;
   } else {
-    return launch(k_rows_mfma_wide<kWideWaves, kWideRG, EPI>, dim3(blocks / (2 * kWideRG)),
-                  dim3(64 * kWideWaves * kWideRG), 0, s, a);
+    return launch(k_rows_mfma_wide<kWideWaves, kWideRG, EPI, NORM>,
+                  dim3(blocks / (2 * kWideRG)), dim3(64 * kWideWaves * kWideRG), 0, s, a);
   }
 }
 
 template <int TP, int EPI, bool NORM>
 int rows_launch_tp(const RowsArgs& a, unsigned blocks, hipStream_t s) {
   const int wv = rows_waves<TP>(a.in / kStep, NORM);
-  const bool mfma = TP == 8 && a.out <= kMfmaMaxOut;
-  if constexpr (TP == 8 && NORM && EPI != kEpiResidual)
-    if (mfma && wv == kWideWaves && blocks >= kWideMinGroups && blocks % (2 * kWideRG) == 0)
-      return rows_launch_wide<EPI>(a, blocks, s);
+  const bool wide = EPI != kEpiResidual && wv == kWideWaves && blocks >= kWideMinGroups &&
+                    blocks % (2 * kWideRG) == 0;
+  const bool mfma = TP == 8 && a.in <= kMfmaMaxIn && (a.out <= kMfmaMaxOut || wide);
+  if constexpr (TP == 8)
+    if (mfma && wide) return rows_launch_wide<EPI, NORM>(a, blocks, s);
 #define LLMK_ROWS_LAUNCH(W)                                                                     \
   if constexpr (TP == 8)                                                                        \
     if (mfma)                                                                                   \

@@ -69,12 +69,13 @@ def test_linear_matches_oracle(llmk, orc, blas, T, K, N):
 
 
 @pytest.mark.parametrize("K,N", [(2048, 3072), (2048, 2048), (8192, 2048), (512, 1000),
-                                 (2048, 16384), (1024, 13)])
+                                 (2048, 16384), (2048, 20480), (1024, 13)])
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8])
 def test_linear_rows_matches_oracle(llmk, orc, T, K, N):
-    """The few-rows kernel (T <= 8): every row count of each padded width (1, 2, 4, 8), output
-    widths that are not multiples of the kernel's 8 rows per block, and in_features over several
-    steps per wave (8192)."""
+    """The few-rows kernels (T <= 8): every row count of each padded width (1, 2, 4, 8), output
+    widths that are not multiples of the kernel's 8 rows per block, in_features over several
+    steps per wave (8192), and at 5 to 8 rows the matrix-core kernels (2048 x 20480: the wide
+    one above 16384 outputs)."""
     rng = np.random.default_rng(0x5EED0210 + 16 * T + K // 512)
     x = normal_f16(rng, (T, K))
     w = normal_f16(rng, (N, K), std=0.02)
@@ -206,8 +207,9 @@ def test_linear_rows_wide_normalising_launches_give_the_bits_of_the_separate_lau
     """Normalising few-rows launches with at least 2048 groups of 8 output rows (gate/up at
     in = 2048; at 5 to 8 rows the 16-wave blocks that stage x in LDS once per 64 rows) against
     RMSNorm + the plain few-rows projection + the separate epilogue: every output bit, for the
-    plain store, the SwiGLU epilogue and the RoPE / K/V scatter epilogue (240 query heads, so
-    that the QKV rows reach 2048 groups). T = 3 takes the dot-product kernel for both."""
+    plain store (16384 and 20480 outputs), the SwiGLU epilogue and the RoPE / K/V scatter
+    epilogue (240 query heads, so that the QKV rows reach 2048 groups). T = 3 takes the
+    dot-product kernel for both."""
     rng = np.random.default_rng(0x5EED0250 + T)
     H, eps, inter = 2048, 1e-5, 8192
     x = dev(normal_f16(rng, (T, H)))
@@ -225,6 +227,16 @@ def test_linear_rows_wide_normalising_launches_give_the_bits_of_the_separate_lau
     bad, exact = linear_rule(host(y2), orc.linear(host(normed), host(wgu), T, H, 2 * inter,
                                                   threads=16).ravel())
     assert bad == 0 and exact > 0.9
+
+    print(f"wide few-rows T={T}: store above 16384 outputs", flush=True)
+    N = 20480
+    w = dev(normal_f16(rng, (N, H), std=0.02))
+    z1 = torch.full((T * N,), float("nan"), dtype=torch.float16, device=DEV)
+    z2 = z1.clone()
+    llmk.linear_rows_norm(x, nw, eps, w, z1, T, H, N)
+    llmk.linear_rows(normed, w, z2, T, H, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(z1), host(z2))
 
     print(f"wide few-rows T={T}: swiglu", flush=True)
     act1 = torch.full((T * inter,), float("nan"), dtype=torch.float16, device=DEV)
