@@ -587,9 +587,9 @@ __global__ void __launch_bounds__(64 * WV) k_rows_mfma(RowsArgs a) {
 //     (global_load_lds_dwordx4: no registers held while they are in flight).
 //   - Each wave streams 16 W rows (two row groups) of its step into registers: 16 KiB in flight
 //     per wave, 256 KiB per CU with one block per CU, the one-row kernel's figure.
-//   - NORM: row t's sum of squares is taken by wave t in the RMSNorm kernel's order and the
-//     block's x is normalised in place in LDS once. The products, the waves' sums and the
-//     epilogues are those of k_rows_mfma: every output has k_rows_mfma's bits.
+//   - NORM: wave t takes row t's sum of squares in the RMSNorm kernel's order and writes the
+//     row back normalised, once per block. The products, the waves' sums and the epilogues are
+//     those of k_rows_mfma: every output has k_rows_mfma's bits.
 // The compiler cannot tell which outstanding loads an LDS read after global_load_lds depends on
 // and waits for all of them (s_waitcnt vmcnt(0)) at an LDS fence, which would hold the barriers
 // until every W load had landed. So each wave waits for exactly its own DMA loads (issued before
@@ -620,7 +620,6 @@ __global__ void __launch_bounds__(64 * WV * RG, 1) k_rows_mfma_wide(RowsArgs a) 
   static_assert(NW <= 16 && NW >= TP, "one wave per row's sum of squares");
   static_assert(EPI != kEpiResidual, "the residual epilogue keeps the narrow kernels");
   __shared__ float part[RG * G][WV][kRows * TPP];
-  __shared__ float inv_s[TP];
   __shared__ u32x4 xs[TP][WV][64];
   __shared__ u32x4 nws[WV][64];
   const int lane = threadIdx.x & 63;
@@ -664,12 +663,16 @@ __global__ void __launch_bounds__(64 * WV * RG, 1) k_rows_mfma_wide(RowsArgs a) 
   wait_vm_lgkm<NWL, 15>();  // this wave's DMA loads have landed; its W loads stay in flight
   dma_barrier();
   if constexpr (NORM) {
+    // Wave t takes row t: its sum of squares, then the row normalised in place from the slices
+    // it already holds (no second pass over LDS, one barrier).
     if (wave < TP) {
       const int t = wave;
+      u32x4 xr[WV];
       float ss = 0.0f;
 #pragma unroll
       for (int k = 0; k < WV; ++k) {
-        const f16x8 h = as_h8(xs[t][k][lane]);
+        xr[k] = xs[t][k][lane];
+        const f16x8 h = as_h8(xr[k]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float f = (float)h[j];
@@ -677,18 +680,15 @@ __global__ void __launch_bounds__(64 * WV * RG, 1) k_rows_mfma_wide(RowsArgs a) 
         }
       }
       ss = wave_sum(ss);
-      if (lane == 0) inv_s[t] = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
-    }
-    wait_vm_lgkm<63, 0>();
-    dma_barrier();
-    for (int i = wave; i < TP * WV; i += NW) {
-      const int t = i / WV, k = i % WV;
-      const f16x8 h = as_h8(xs[t][k][lane]);
-      const float inv = inv_s[t];
-      f16x8 an;
+      const float inv = 1.0f / __builtin_sqrtf(ss / (float)in + a.eps);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
-      xs[t][k][lane] = as_u4(as_h8(nws[k][lane]) * an);
+      for (int k = 0; k < WV; ++k) {
+        const f16x8 h = as_h8(xr[k]);
+        f16x8 an;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) an[j] = (f16)((float)h[j] * inv);
+        xs[t][k][lane] = as_u4(as_h8(nws[k][lane]) * an);
+      }
     }
     wait_vm_lgkm<63, 0>();
     dma_barrier();
