@@ -59,7 +59,7 @@ SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_819
             "argmax", "step_256", "step_8", "sched", "probe_sweep", "probe_kernels", "copy_1GiB",
             "residual_add", "rmsnorm_8192", "kv_scatter_8192", "kv_scatter_batch_256",
             "pass2_graph", "pass2_layers", "pass_fused", "pass2_fused", "calib", "calib_resident",
-            "calib_hbm", "end", "setup"]
+            "calib_hbm", "end", "setup", "sched_ab"]
 
 # Launch shapes (blocks, threads) of the 16-layer pass at 256 sequences, from the launchers'
 # grid rules: the embedding and add+RMSNorm take one 64-thread wave per row below 4096 rows
@@ -1548,6 +1548,7 @@ class Bench:
         # host (the reference's default: logits copied back, converted, searched) and on the
         # GPU; three rounds, the order of the four reversed every other round; per decode step
         # the time split of llmk_step_times (ref: engine/batched.h:6-11).
+        self.mark("sched_ab")  # kept apart: host-argmax passes end without an argmax kernel
         ab_reqs = [dict(r, arrival_step=0) for r in reqs]
         cfgs = [("batched, CPU argmax", wl.SCHED_MAX_RUNNING, 1),
                 ("batched, GPU argmax", wl.SCHED_MAX_RUNNING, 0),
