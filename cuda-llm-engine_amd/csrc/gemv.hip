@@ -763,8 +763,10 @@ int rows_launch_wide(const RowsArgs& a, unsigned blocks, hipStream_t s) {
 template <int TP, int EPI, bool NORM>
 int rows_launch_tp(const RowsArgs& a, unsigned blocks, hipStream_t s) {
   const int wv = rows_waves<TP>(a.in / kStep, NORM);
-  const bool wide = EPI != kEpiResidual && wv == kWideWaves && blocks >= kWideMinGroups &&
-                    blocks % (2 * kWideRG) == 0;
+  // exactly kWideWaves steps: the wide kernel gives every wave one step (without the norm,
+  // rows_waves rounds 3 steps up to 4 waves)
+  const bool wide = EPI != kEpiResidual && wv == kWideWaves && a.in == kWideWaves * kStep &&
+                    blocks >= kWideMinGroups && blocks % (2 * kWideRG) == 0;
   const bool mfma = TP == 8 && a.in <= kMfmaMaxIn && (a.out <= kMfmaMaxOut || wide);
   if constexpr (TP == 8)
     if (mfma && wide) return rows_launch_wide<EPI, NORM>(a, blocks, s);

@@ -69,13 +69,13 @@ def test_linear_matches_oracle(llmk, orc, blas, T, K, N):
 
 
 @pytest.mark.parametrize("K,N", [(2048, 3072), (2048, 2048), (8192, 2048), (512, 1000),
-                                 (2048, 16384), (2048, 20480), (1024, 13)])
+                                 (2048, 16384), (2048, 20480), (1536, 16384), (1024, 13)])
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8])
 def test_linear_rows_matches_oracle(llmk, orc, T, K, N):
     """The few-rows kernels (T <= 8): every row count of each padded width (1, 2, 4, 8), output
     widths that are not multiples of the kernel's 8 rows per block, in_features over several
     steps per wave (8192), and at 5 to 8 rows the matrix-core kernels (2048 x 20480: the wide
-    one above 16384 outputs)."""
+    one above 16384 outputs; 1536 x 16384: three steps, which the wide kernel must not take)."""
     rng = np.random.default_rng(0x5EED0210 + 16 * T + K // 512)
     x = normal_f16(rng, (T, K))
     w = normal_f16(rng, (N, K), std=0.02)
