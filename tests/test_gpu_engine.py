@@ -69,13 +69,16 @@ def test_linear_matches_oracle(llmk, orc, blas, T, K, N):
 
 
 @pytest.mark.parametrize("K,N", [(2048, 3072), (2048, 2048), (8192, 2048), (512, 1000),
-                                 (2048, 16384), (2048, 20480), (1536, 16384), (1024, 13)])
+                                 (2048, 16384), (2048, 20480), (2048, 16392), (1536, 16384),
+                                 (1024, 13)])
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8])
 def test_linear_rows_matches_oracle(llmk, orc, T, K, N):
     """The few-rows kernels (T <= 8): every row count of each padded width (1, 2, 4, 8), output
     widths that are not multiples of the kernel's 8 rows per block, in_features over several
     steps per wave (8192), and at 5 to 8 rows the matrix-core kernels (2048 x 20480: the wide
-    one above 16384 outputs; 1536 x 16384: three steps, which the wide kernel must not take)."""
+    one above 16384 outputs; 2048 x 16392: above 16384 outputs in groups the wide kernel does
+    not tile, so the dot products; 1536 x 16384: three steps, which the wide kernel must not
+    take)."""
     rng = np.random.default_rng(0x5EED0210 + 16 * T + K // 512)
     x = normal_f16(rng, (T, K))
     w = normal_f16(rng, (N, K), std=0.02)
@@ -201,7 +204,7 @@ def test_linear_rows_fused_give_the_bits_of_the_separate_launches(llmk, orc, T):
     assert int((host(pools[0]) != POISON).sum()) == T * kvdim  # one row per token, no more
 
 
-@pytest.mark.parametrize("T", [3, 5, 8])
+@pytest.mark.parametrize("T", [3, 5, 7, 8])
 def test_linear_rows_wide_normalising_launches_give_the_bits_of_the_separate_launches(llmk, orc,
                                                                                        T):
     """Normalising few-rows launches with at least 2048 groups of 8 output rows (gate/up at
