@@ -72,6 +72,20 @@ def test_config3_rope_8192_tokens(llmk, orc, wl, inv):
     assert_tol(ck, 0.995, "config 3 K")
 
 
+def test_config3_rope_position_zero_is_the_identity(llmk, wl, inv):
+    """A size-independent property at config 3's full size: with every position 0, cos = 1 and
+    sin = 0, so x1' = fp16(r16(x1) - r16(x2 * 0)) = x1 for finite inputs and Q and K keep every
+    bit. (The oracle comparison above covers the other positions.)"""
+    d = wl.rope_inputs(inv_freq=inv[1])
+    d["positions"].zero_()
+    q0, k0 = d["q"].clone(), d["k"].clone()
+    llmk.rope_apply(d["q"], d["k"], d["positions"], d["inv_freq"], d["T"], d["nh"], d["nkv"],
+                    d["hd"])
+    torch.cuda.synchronize()
+    assert torch.equal(d["q"].view(torch.int16), q0.view(torch.int16))
+    assert torch.equal(d["k"].view(torch.int16), k0.view(torch.int16))
+
+
 def test_config4_swiglu_8192x8192(llmk, orc, wl):
     d = wl.swiglu_inputs()
     g, u = host(d["gate"]), host(d["up"])
