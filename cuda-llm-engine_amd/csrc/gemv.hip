@@ -24,9 +24,9 @@
 //     there instead of every wave re-reading whole rows.
 //   - Launches of 5 to 8 rows of matrices of at most kMfmaMaxOut x kMfmaMaxIn run the same
 //     blocks on the matrix cores instead (k_rows_mfma, v_mfma_f32_4x4x4_16b_f16;
-//     rows_launch_tp says why), and
-//     normalising ones with many output rows (gate/up) run 16-wave blocks that stage x once per
-//     64 rows through direct-to-LDS loads (k_rows_mfma_wide).
+//     rows_launch_tp says why), and those with many output rows at in = 2048 (gate/up, the
+//     lm head) run 16-wave blocks that stage x once per 64 rows through direct-to-LDS loads
+//     (k_rows_mfma_wide).
 //   - A residual epilogue reads the value it adds to at the start of the kernel, not after the
 //     products (0.25-0.3 us per launch on the o and down shapes at every row count).
 // Summation order differs from cuBLAS/hipBLASLt (lane-strided partial sums, then the butterfly),
