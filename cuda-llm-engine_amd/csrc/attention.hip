@@ -46,14 +46,6 @@ constexpr float kScoreScale = 0.125f * 1.44269504088896341f;
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-// Element k of a 4 x 32-bit vector as a scalar. (The element is copied out before any
-// __builtin_bit_cast: this compiler lowers a bit_cast applied directly to a vector-element
-// expression as a read of element 0.)
-__device__ __forceinline__ uint32_t elem(u32x4 v, int k) {
-  const uint32_t e = v[k];
-  return e;
-}
-
 // Partial dot product of 8 fp16 dims (4 packed pairs), fp32 accumulation.
 __device__ __forceinline__ float dot8(u32x4 a, u32x4 b) {
   float s = 0.0f;

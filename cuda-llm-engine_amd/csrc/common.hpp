@@ -42,6 +42,14 @@ __device__ __forceinline__ void st16_stream(void* p, u32x4 v) {
 __device__ __forceinline__ f16x8 as_h8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 __device__ __forceinline__ u32x4 as_u4(f16x8 v) { return __builtin_bit_cast(u32x4, v); }
 
+// Element k of a 4 x 32-bit vector as a scalar. Copy an element out this way before any
+// __builtin_bit_cast: this compiler (ROCm 7.2 clang) lowers a bit_cast applied directly to a
+// vector-element expression (v[k]) as a read of element 0, whatever k is.
+__device__ __forceinline__ uint32_t elem(u32x4 v, int k) {
+  const uint32_t e = v[k];
+  return e;
+}
+
 // ---------------------------------------------------------------------------------------------
 // wave64 reduction. The first four steps run on DPP lane permutes (no LDS traffic); after them
 // every lane of each 16-lane row holds that row's sum, and the four row sums are combined as

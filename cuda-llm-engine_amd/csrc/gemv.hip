@@ -44,11 +44,6 @@ constexpr int kStep = 512;    // in elements per wave step: 64 lanes x 8 halves
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t elem(u32x4 v, int k) {
-  const uint32_t e = v[k];
-  return e;
-}
-
 // acc + the dot product of 8 fp16 pairs, fp32 accumulation.
 __device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
 #pragma unroll
