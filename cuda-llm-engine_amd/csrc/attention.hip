@@ -539,17 +539,31 @@ __device__ __forceinline__ int block_scan(int v, int* red, int* total) {
 // longer batches read the lengths a second time.
 constexpr int kPrologueTiles = 4;
 
-// Page-balanced grid (blocks, kv groups): the pages of all sequences, laid end to end in
-// sequence order (T of them), are cut into runs of q = max(ceil(T / blocks), q_min) pages and
-// block b takes run b, whatever sequences it spans. Every block gets the same amount of work,
-// so one resident round of blocks ends together. Each (sequence, block) piece is a segment; a
-// sequence whose pages start at global page g_s has segments in blocks g_s / q ..
-// (g_s + P_s - 1) / q, and its k-th segment leaves its partial in workspace slot k. q_min =
-// ceil((P_max - 1) / (num_splits - 2)) over the batch's largest page count P_max keeps that
-// count at most num_splits - 1, so slot num_splits - 1 of every sequence is free: the block
-// holding a sequence's first segment records there how many segments it has. A sequence with a
-// single segment gets its output written here; the merge kernel finishes the others and writes
-// the NaN of empty sequences.
+// The cost of starting a sequence inside a block's run, in pages of KVW kv heads. Switching
+// to a new sequence costs a block about 4 us (per-block timestamps, 256 sequences of lengths
+// uniform in [1, 2048], 8 kv heads: the first fold of a segment 1.9 us after its start, the
+// waves' LDS merge 1.7 us, the stores and the tail chunk 0.7 us), the time it takes to stream
+// about 4 pages of 8 kv heads; narrower rows stream their pages faster, so a start weighs
+// proportionally more pages. Cutting runs by pages alone left the blocks holding 4 segments
+// 12 us behind those holding one; with starts counted, block end times no longer depend on the
+// segment count (same box, 256 of U[1, 2048]: 95.2 -> 92.0 us, both kernels; 3 and 5 units
+// measured within 0.3 us of 4).
+template <int KVW>
+constexpr int start_units() { return 32 / KVW; }
+
+// Page-balanced grid (blocks, kv groups). The sequences are laid end to end in sequence order
+// as units of work: a sequence with P > 0 pages takes kStartUnits<KVW> units for its start
+// followed by one unit per page (U units in all). The units are cut into runs of
+// q = max(ceil(U / blocks), q_min) and block b takes run b, whatever sequences it spans: the
+// pages of a sequence whose units fall in the run, and none for a start unit. Every block gets
+// the same amount of work, starts included, so one resident round of blocks ends together. Each
+// (sequence, block) piece is a segment; a sequence whose page 0 sits at unit r_s has segments in
+// blocks r_s / q .. (r_s + P_s - 1) / q, and its k-th segment leaves its partial in workspace
+// slot k. q_min = ceil((P_max - 1) / (num_splits - 2)) over the batch's largest page count
+// P_max keeps that count at most num_splits - 1, so slot num_splits - 1 of every sequence is
+// free: the block holding a sequence's first segment records there how many segments it has. A
+// sequence with a single segment gets its output written here; the merge kernel finishes the
+// others and writes the NaN of empty sequences.
 // Argument order as in k_attn_split: what the prologue needs first sits in the preloaded dwords.
 template <int KVW>
 __global__ void __launch_bounds__(kThreads)
@@ -564,36 +578,37 @@ k_attn_balanced(const int* __restrict__ seq_lens, const int* __restrict__ block_
   const int b = blockIdx.x, kvg = blockIdx.y, tid = threadIdx.x;
 
   // Page counts: thread t holds sequences t, t + kThreads, ... (the first kPrologueTiles).
+  constexpr int C = start_units<KVW>();
   const bool held = n_seq <= kPrologueTiles * kThreads;
   int pv[kPrologueTiles];
-  int mine = 0, pmax = 0;
+  int mine = 0, pmax = 0;  // units of the thread's sequences, their largest page count
 #pragma unroll
   for (int t = 0; t < kPrologueTiles; ++t) {
     const int s = t * kThreads + tid;
     pv[t] = s < n_seq ? seq_pages(seq_lens[s], max_pages) : 0;
-    mine += pv[t];
+    mine += pv[t] > 0 ? C + pv[t] : 0;
     pmax = pv[t] > pmax ? pv[t] : pmax;
   }
   if (!held)
     for (int s = kPrologueTiles * kThreads + tid; s < n_seq; s += kThreads) {
       const int P = seq_pages(seq_lens[s], max_pages);
-      mine += P;
+      mine += P > 0 ? C + P : 0;
       pmax = P > pmax ? P : pmax;
     }
-  int T, P_max;
-  block_sum_max(mine, red, &T, &P_max);
-  const int per = (T + n_blocks - 1) / n_blocks;  // n_blocks == gridDim.x, passed in SGPRs
+  int U, P_max;
+  block_sum_max(mine, red, &U, &P_max);
+  const int per = (U + n_blocks - 1) / n_blocks;  // n_blocks == gridDim.x, passed in SGPRs
   const int q_min = P_max > 1 ? (P_max - 1 + num_splits - 3) / (num_splits - 2) : 1;
   const int qp = per > q_min ? per : q_min;
-  const long long g0l = (long long)b * qp;
-  if (g0l >= T) return;
-  const int g0 = (int)g0l;
-  const int g1 = g0 + qp < T ? g0 + qp : T;
+  const long long u0l = (long long)b * qp;
+  if (u0l >= U) return;
+  const int u0 = (int)u0l;
+  const int u1 = u0 + qp < U ? u0 + qp : U;
 
-  // The sequence holding global page g0, and where its pages start.
+  // The sequence holding unit u0, and its first unit.
   int running = 0;
   const int tiles = (n_seq + kThreads - 1) / kThreads;
-  for (int t = 0; t < tiles && running <= g0; ++t) {
+  for (int t = 0; t < tiles && running <= u0; ++t) {
     const int s = t * kThreads + tid;
     int P = 0;
     if (held) {
@@ -602,42 +617,49 @@ k_attn_balanced(const int* __restrict__ seq_lens, const int* __restrict__ block_
     } else {
       P = s < n_seq ? seq_pages(seq_lens[s], max_pages) : 0;
     }
+    const int E = P > 0 ? C + P : 0;
     int tile;
-    const int incl = running + block_scan(P, red, &tile);
-    if (P > 0 && incl - P <= g0 && g0 < incl) {
+    const int incl = running + block_scan(E, red, &tile);
+    if (E > 0 && incl - E <= u0 && u0 < incl) {
       found[0] = s;
-      found[1] = incl - P;
+      found[1] = incl - E;
     }
     running += tile;
   }
   __syncthreads();
-  int s = found[0], gs = found[1];
+  int s = found[0], us = found[1];
 
   const int h = kvg * MergeLds<KVW>::HEADS + (tid >> 3);
   const bool writer = (tid >> 3) < MergeLds<KVW>::HEADS && h < n_heads;
-  while (gs < g1) {
+  while (us < u1) {
     const int S = seq_lens[s];
     const int P = seq_pages(S, max_pages);
     if (P > 0) {
-      const int lp0 = (g0 > gs ? g0 : gs) - gs, lp1 = (g1 < gs + P ? g1 : gs + P) - gs;
-      const int pos1 = S < lp1 * kPage ? S : lp1 * kPage;
-      float A[8], M, L;
-      u32x4 qv[kGroup];
-      load_query<KVW>(qv, q, s, kvg, n_heads);
-      attend_segment<KVW>(qv, k_pool, v_pool, TablePages{block_tables + (size_t)s * max_pages},
-                          lp0 * kPage, pos1, kvg, n_kv_heads, lds, A, M, L);
-      const int first = gs / qp, n_seg = (gs + P - 1) / qp - first + 1, k = b - first;
-      if (writer) {
-        if (n_seg == 1)
-          store_out(out, s, h, n_heads, A, L);
-        else
-          store_partial(part_o, part_ml, ((size_t)s * num_splits + k) * n_heads + h, A, M, L);
+      const int r = us + C;  // the unit of the sequence's page 0
+      const int a0 = u0 > r ? u0 : r, a1 = u1 < r + P ? u1 : r + P;
+      if (a0 < a1) {  // the run holds some of its pages, not only its start
+        const int lp0 = a0 - r, lp1 = a1 - r;
+        const int pos1 = S < lp1 * kPage ? S : lp1 * kPage;
+        float A[8], M, L;
+        u32x4 qv[kGroup];
+        load_query<KVW>(qv, q, s, kvg, n_heads);
+        attend_segment<KVW>(qv, k_pool, v_pool,
+                            TablePages{block_tables + (size_t)s * max_pages}, lp0 * kPage, pos1,
+                            kvg, n_kv_heads, lds, A, M, L);
+        const int first = r / qp, n_seg = (r + P - 1) / qp - first + 1, k = b - first;
+        if (writer) {
+          if (n_seg == 1)
+            store_out(out, s, h, n_heads, A, L);
+          else
+            store_partial(part_o, part_ml, ((size_t)s * num_splits + k) * n_heads + h, A, M,
+                          L);
+        }
+        if (k == 0 && tid == 0)
+          part_ml[((size_t)s * num_splits + num_splits - 1) * n_heads] =
+              make_float2(__builtin_bit_cast(float, n_seg), 0.0f);
       }
-      if (k == 0 && tid == 0)
-        part_ml[((size_t)s * num_splits + num_splits - 1) * n_heads] =
-            make_float2(__builtin_bit_cast(float, n_seg), 0.0f);
+      us += C + P;
     }
-    gs += P;
     ++s;
   }
 }
