@@ -1657,6 +1657,42 @@ def cpu_decode_pass(h, lib, wl, P, i32, f32):
     return make
 
 
+def summary(kernels: dict, torch, dev, K: int, W: int) -> None:
+    """The run's headline figures, a few lines at the very end of stderr (a reader that keeps
+    only the tail of the log still gets every configuration's time and roofline fraction)."""
+    p = torch.cuda.get_device_properties(dev)
+    log(f"summary: {p.name} ({getattr(p, 'gcnArchName', '?')}, {p.multi_processor_count} CUs), "
+        f"steps={K} warmup={W}; us = event-timed mean per launch, % of 8 TB/s")
+    rows = [("config 2 add+RMSNorm [8192,2048]", "add_rmsnorm_8192x2048"),
+            ("config 3 RoPE 8192 tokens", "rope_8192"),
+            ("config 4a SwiGLU [8192,8192]", "swiglu_8192x8192"),
+            ("config 4b embedding 8192 ids", "embedding_8192"),
+            ("config 1 RMSNorm [16,2048]", "rmsnorm_16x2048"),
+            ("config 5 pass, one launch", "decode_pass_16x256_fused"),
+            ("config 5 pass, per layer", "decode_pass_16x256_layers"),
+            ("config 5 pass, op by op", "decode_pass_16x256"),
+            ("attention 256 of U[1,2048]", "attention_decode_256"),
+            ("attention 16 x 2048", "attention_decode_16x2048"),
+            ("argmax [256,128256]", "argmax_256x128256"),
+            ("residual add [8192,2048]", "residual_add_8192x2048"),
+            ("RMSNorm [8192,2048]", "rmsnorm_8192x2048"),
+            ("decode step 1B, 256 rows", "decode_step_1b_256"),
+            ("decode step 1B, 8 rows", "decode_step_1b_8"),
+            ("copy probe 1 GiB", "copy_1GiB")]
+    for label, key in rows:
+        e = kernels.get(key)
+        if not e or e.get("us_mean") is None:
+            continue
+        ceil = e.get("ceiling") or {}
+        extra = (f", {100 * ceil['kernel_frac_of_ceiling']:.1f}% of its {ceil['mix']} ceiling"
+                 if ceil.get("kernel_frac_of_ceiling") else "")
+        log(f"  {label:34s} {e['us_mean']:9.2f} us {100 * e['frac_of_peak']:5.1f}%{extra}")
+    s = kernels.get("scheduler_24x32_1b")
+    if s and s.get("words_per_s"):
+        log(f"  {'scheduler, 24 requests':34s} {s['words_per_s']:9.1f} words/s up to 8 at once, "
+            f"{s['words_per_s_one_at_a_time']:.1f} one at a time")
+
+
 def main() -> int:
     args = parse_args()
     if args.summarize_profiles:
@@ -1720,6 +1756,7 @@ def main() -> int:
             cpu = {k: v for k, v in head_cpu.items() if k != "gpu_over_cpu"}
             cpu.update(b.cpu_info)
 
+    summary(b.kernels, torch, b.dev, K, W)
     head = b.kernels["add_rmsnorm_8192x2048"]
     value = nbytes * K / t_head["wall_s"] / 1e9
     rec = {
