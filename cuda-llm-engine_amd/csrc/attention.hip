@@ -574,18 +574,19 @@ k_attn_balanced(const int* __restrict__ seq_lens, const int* __restrict__ block_
                 float* __restrict__ part_o, float2* __restrict__ part_ml) {
   __shared__ MergeLds<KVW> lds;
   __shared__ int red[2 * kWaves];
-  __shared__ int found[2];
+  __shared__ int found[3];
   const int b = blockIdx.x, kvg = blockIdx.y, tid = threadIdx.x;
 
   // Page counts: thread t holds sequences t, t + kThreads, ... (the first kPrologueTiles).
   constexpr int C = start_units<KVW>();
   const bool held = n_seq <= kPrologueTiles * kThreads;
-  int pv[kPrologueTiles];
+  int lv[kPrologueTiles], pv[kPrologueTiles];  // lengths and page counts
   int mine = 0, pmax = 0;  // units of the thread's sequences, their largest page count
 #pragma unroll
   for (int t = 0; t < kPrologueTiles; ++t) {
     const int s = t * kThreads + tid;
-    pv[t] = s < n_seq ? seq_pages(seq_lens[s], max_pages) : 0;
+    lv[t] = s < n_seq ? seq_lens[s] : 0;
+    pv[t] = seq_pages(lv[t], max_pages);
     mine += pv[t] > 0 ? C + pv[t] : 0;
     pmax = pv[t] > pmax ? pv[t] : pmax;
   }
@@ -605,34 +606,39 @@ k_attn_balanced(const int* __restrict__ seq_lens, const int* __restrict__ block_
   const int u0 = (int)u0l;
   const int u1 = u0 + qp < U ? u0 + qp : U;
 
-  // The sequence holding unit u0, and its first unit.
+  // The sequence holding unit u0, its first unit and its length.
   int running = 0;
   const int tiles = (n_seq + kThreads - 1) / kThreads;
   for (int t = 0; t < tiles && running <= u0; ++t) {
     const int s = t * kThreads + tid;
-    int P = 0;
+    int S = 0;
     if (held) {
 #pragma unroll
-      for (int u = 0; u < kPrologueTiles; ++u) P = u == t ? pv[u] : P;
+      for (int u = 0; u < kPrologueTiles; ++u) S = u == t ? lv[u] : S;
     } else {
-      P = s < n_seq ? seq_pages(seq_lens[s], max_pages) : 0;
+      S = s < n_seq ? seq_lens[s] : 0;
     }
+    const int P = seq_pages(S, max_pages);
     const int E = P > 0 ? C + P : 0;
     int tile;
     const int incl = running + block_scan(E, red, &tile);
     if (E > 0 && incl - E <= u0 && u0 < incl) {
       found[0] = s;
       found[1] = incl - E;
+      found[2] = S;
     }
     running += tile;
   }
   __syncthreads();
-  int s = found[0], us = found[1];
+  int s = __builtin_amdgcn_readfirstlane(found[0]), us = __builtin_amdgcn_readfirstlane(found[1]);
+  int S = __builtin_amdgcn_readfirstlane(found[2]);
 
   const int h = kvg * MergeLds<KVW>::HEADS + (tid >> 3);
   const bool writer = (tid >> 3) < MergeLds<KVW>::HEADS && h < n_heads;
   while (us < u1) {
-    const int S = seq_lens[s];
+    // The next sequence's length, read while this one is attended: a new segment then starts
+    // with its query and table reads, one round trip sooner.
+    const int S_next = s + 1 < n_seq ? seq_lens[s + 1] : 0;
     const int P = seq_pages(S, max_pages);
     if (P > 0) {
       const int r = us + C;  // the unit of the sequence's page 0
@@ -660,6 +666,7 @@ k_attn_balanced(const int* __restrict__ seq_lens, const int* __restrict__ block_
       }
       us += C + P;
     }
+    S = S_next;
     ++s;
   }
 }
