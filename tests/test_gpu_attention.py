@@ -267,6 +267,28 @@ def test_decode_batch_of_256_sequences_up_to_2048(llmk, orc):
         assert_tol(orc.compare(d.run(llmk, splits), ref), EXACT_FLOOR, f"batch 256 splits {splits}")
 
 
+@pytest.mark.parametrize("nkv", [1, 2, 4, 8, 16])
+def test_page_balanced_runs_weigh_sequence_starts(llmk, orc, nkv):
+    """The page-balanced grid cuts units of work, not pages: a sequence's start weighs 32 / KVW
+    pages. With 1 or 2 kv heads per row (a start worth 32 or 16 pages) and many one- to
+    three-page sequences, whole runs fall on start units and hold no page, runs end inside a
+    start, and a sequence's page 0 opens a run; 16 kv heads take two kv groups of blocks. Empty
+    sequences sit in between."""
+    rng = np.random.default_rng(0xB1A5 + nkv)
+    lens = rng.integers(1, 49, 400)
+    lens[rng.choice(400, 40, replace=False)] = 0
+    lens[::97] = 2048 // nkv  # a few long ones, split over several runs
+    c = attention_case(rng, lens, n_heads=4 * nkv, n_kv_heads=nkv)
+    d = OnDevice(c)
+    ref = oracle_out(orc, c).reshape(400, -1)
+    empty = c["lens"] <= 0
+    for splits in (3, 8, 32):
+        got = d.run(llmk, splits).reshape(400, -1)
+        assert np.all(np.isnan(got[empty].view(np.float16))), f"n_kv {nkv} splits {splits}"
+        assert_tol(orc.compare(got[~empty].reshape(-1), ref[~empty].reshape(-1)), EXACT_FLOOR,
+                   f"n_kv {nkv} splits {splits}")
+
+
 def test_many_short_sequences_share_a_block(llmk, orc):
     """Page-balanced runs that cover many whole sequences and pieces of others: 300 sequences
     of 1 to 40 positions, plus runs of a single page (every length <= 16, max_pages 1)."""
