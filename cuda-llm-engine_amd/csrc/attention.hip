@@ -892,19 +892,7 @@ k_attn_merge_many(const float* __restrict__ part_o, const float2* __restrict__ p
 // sequences split into twice the pieces and each block switches segments twice as often
 // (same box: 256 of U[1, 2048] 100.1 -> 98.9 us with one block per CU, 64 x 2048
 // 50.3 -> 48.5, 256 x 2048 172.6 -> 168.4; one 8-wave block per CU 101.2 / 50.2 / 170.9).
-int balanced_blocks() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  const int known = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
-  if (known > 0) return known;
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus <= 0)
-    return 0;
-  __atomic_store_n(&cache[dev], cus, __ATOMIC_RELAXED);
-  return cus;
-}
+int balanced_blocks() { return device_cus(); }
 
 struct AttnArgs {
   const f16 *q, *k_pool, *v_pool;

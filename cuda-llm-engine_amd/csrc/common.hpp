@@ -111,4 +111,20 @@ __device__ __forceinline__ void lds_barrier() {
 
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
+// The current device's CU count, read once per device (0 if it cannot be read). Launch shapes
+// that size a grid to one resident round of blocks use it.
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  const int known = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+  if (known > 0) return known;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 0;
+  __atomic_store_n(&cache[dev], cus, __ATOMIC_RELAXED);
+  return cus;
+}
+
 }  // namespace llmk

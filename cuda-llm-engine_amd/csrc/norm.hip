@@ -60,6 +60,73 @@ k_rmsnorm_wave(const f16* x, f16* resid, const f16* __restrict__ w, f16* out, in
                                 eps, threadIdx.x & 63);
 }
 
+// RMSNorm of 2048-wide rows, R rows per wave (waves of 4 per block). Wave w of the grid's
+// `stride` waves takes rows w, w + stride, ..., w + (R - 1) * stride; it issues every load of
+// its R rows (R x 4 vectors per lane, twice that FUSED) before the first row's sum, so load
+// instruction r of all waves covers one contiguous band of `stride` rows. Each row then goes
+// through rmsnorm_row's arithmetic (the residual add, norm_store), so the bits are those of
+// k_rmsnorm_wave. Rows past n_rows load the last row again and store nothing.
+template <int R, bool FUSED>
+__global__ void __launch_bounds__(256)
+k_rmsnorm_rows(const f16* x, f16* resid, const f16* __restrict__ w, f16* out, int n_rows,
+               int stride, float hidden_f, float eps) {
+  constexpr int VPL = 4, VPR = 64 * VPL;
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  f16x8 wv[VPL];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) wv[k] = as_h8(ld16(w + 8 * (lane + 64 * k)));
+  f16x8 h[R][VPL], xv[FUSED ? R : 1][VPL];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = min(wave + r * stride, n_rows - 1);
+    const size_t base = (size_t)row * VPR * 8;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      h[r][k] = as_h8(ld16_stream((FUSED ? resid : x) + base + 8 * (lane + 64 * k)));
+      if (FUSED) xv[FUSED ? r : 0][k] = as_h8(ld16_stream(x + base + 8 * (lane + 64 * k)));
+    }
+  }
+  // Keep the compiler from sinking loads below the first row's arithmetic and stores: the
+  // point is to have all of them in flight at once.
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = wave + r * stride;
+    if (row < n_rows) {
+      const size_t base = (size_t)row * VPR * 8;
+      if (FUSED) {
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+          h[r][k] = h[r][k] + xv[FUSED ? r : 0][k];
+          st16_stream(resid + base + 8 * (lane + 64 * k), as_u4(h[r][k]));
+        }
+      }
+      norm_store<VPL, true>(h[r], wv, out + base, VPR, hidden_f, eps, lane);
+    }
+  }
+}
+
+// Rows per wave for k_rmsnorm_rows, or 0 for the one-row kernel: the grid must fit one resident
+// round of 4 waves per CU, so rows <= R * 4 * CUs, and the batch must be large enough to fill
+// it. Same box, 2048-wide rows, us (one row per wave -> R rows per wave):
+//   RMSNorm, R = 8: 6144 rows 10.08 -> 9.60, 7168 11.34 -> 10.13, 8192 12.68 -> 10.82; 5120
+//     8.38 -> 9.07 and R = 4 at 3072-4096 rows (5.34 -> 6.75, 6.45 -> 6.79) lose.
+//   add + RMSNorm, R = 4: 3072 rows 9.62 -> 8.62, 4096 12.00 -> 10.94; R = 8: 5120 14.70 ->
+//     13.84, 6144 17.38 -> 15.90, 7168 20.18 -> 18.55, 8192 22.76 -> 21.23.
+//   Past one round (9216, 12288, 16384 rows) both lose or tie; so does R = 16 (VGPR spills).
+// The gain is in dispatch: one wave per row is 2048 4-wave blocks at 8192 rows against 256 here.
+static int rmsnorm_rows_per_wave(int n_rows, bool fused) {
+  const long long slots = 4LL * device_cus();
+  if (slots <= 0) return 0;
+  if (fused) {
+    if (n_rows > 2 * slots && n_rows <= 4 * slots) return 4;
+    if (n_rows > 4 * slots && n_rows <= 8 * slots) return 8;
+    return 0;
+  }
+  return n_rows > 5 * slots && n_rows <= 8 * slots ? 8 : 0;
+}
+
 // Wide rows: one 256-thread block per row, two passes over the row.
 template <bool FUSED>
 __global__ void __launch_bounds__(256)
@@ -103,6 +170,17 @@ static int rmsnorm_launch(const f16* x, f16* resid, const f16* w, f16* out, int 
   const int vpr = hidden / 8;
   const float hf = (float)hidden;
   const int vpl = (vpr + 63) / 64;
+  if (vpr == 256) {
+    const int R = rmsnorm_rows_per_wave(n_rows, FUSED);
+    if (R > 0) {
+      const int blocks = (int)ceil_div(ceil_div((size_t)n_rows, (size_t)R), 4);
+      auto go = [&](auto kern) {
+        return launch(kern, dim3(blocks), dim3(256), 0, stream, x, resid, w, out, n_rows,
+                      4 * blocks, hf, eps);
+      };
+      return R == 4 ? go(k_rmsnorm_rows<4, FUSED>) : go(k_rmsnorm_rows<8, FUSED>);
+    }
+  }
   // Few rows: one wave per block so the rows spread over as many CUs as possible.
   const int wpb = n_rows >= 4096 ? 4 : 1;
   const dim3 grid(ceil_div((size_t)n_rows, (size_t)wpb)), block(64 * wpb);

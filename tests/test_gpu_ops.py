@@ -164,6 +164,40 @@ def test_add_rmsnorm(llmk, orc, rows, hidden):
     assert np.all(got[rows] == CANARY)
 
 
+@pytest.mark.parametrize("rows", [3072, 4096, 5000, 6000, 8191, 8192])
+def test_norms_of_many_rows_give_the_bits_of_one_row_per_wave(llmk, rows):
+    """Batches of 2048-wide rows that fill one resident round run several rows per wave (4 at
+    3072-4096 rows, 8 up to 8192, the fused kernel from 3072 rows and RMSNorm alone from 5120);
+    slices of 1024 rows run one row per wave. Every bit of both outputs and of the updated
+    residual must agree, including the partial last wave (5000, 6000, 8191 rows), and nothing
+    past the last row may be written."""
+    hidden = 2048
+    rng = np.random.default_rng(rows)
+    r, x = normal_f16(rng, (rows, hidden)), normal_f16(rng, (rows, hidden))
+    w = normal_f16(rng, hidden, 1.0, 0.1)
+    dx, dw = dev(x).reshape(-1), dev(w)
+    whole = filled((rows + 1) * hidden, CANARY)
+    llmk.rmsnorm(dx, dw, whole, rows, hidden, EPS)
+    sliced = filled(rows * hidden)
+    for r0 in range(0, rows, 1024):
+        n = min(1024, rows - r0)
+        llmk.rmsnorm(dx[r0 * hidden:], dw, sliced[r0 * hidden:], n, hidden, EPS)
+    got = host(whole)
+    assert np.array_equal(got[:rows * hidden], host(sliced)), f"rmsnorm {rows} rows"
+    assert np.all(got[rows * hidden:] == CANARY)
+    d1, d2 = dev(r).reshape(-1), dev(r).reshape(-1)
+    o1, o2 = filled((rows + 1) * hidden, CANARY), filled(rows * hidden)
+    llmk.add_rmsnorm(d1, dx, dw, o1, rows, hidden, EPS)
+    for r0 in range(0, rows, 1024):
+        n = min(1024, rows - r0)
+        llmk.add_rmsnorm(d2[r0 * hidden:], dx[r0 * hidden:], dw, o2[r0 * hidden:], n, hidden,
+                         EPS)
+    assert np.array_equal(host(d1), host(d2)), f"residual {rows} rows"
+    got = host(o1)
+    assert np.array_equal(got[:rows * hidden], host(o2)), f"add_rmsnorm {rows} rows"
+    assert np.all(got[rows * hidden:] == CANARY)
+
+
 def test_add_rmsnorm_equals_residual_add_then_rmsnorm(llmk):
     """The fused kernel writes exactly what the two reference launches write on the GPU."""
     rng = np.random.default_rng(19)
