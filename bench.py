@@ -135,11 +135,12 @@ SECTION_ROWS = 12
 # measured launch shape whose counters are reported; grid sizes follow from the launchers'
 # grid choices at the benchmark shapes.
 PROFILE_SHAPES = [
-    ("add_rmsnorm_8192x2048", "headline", "k_rmsnorm_waveILi4ELb1ELb1E", 8192 * 64, 134221824),
-    # 8192 blocks of 256 threads over 2,097,152 vectors; 4 rows (waves) per block from 4096 rows;
-    # the scatters: one row per wave, 4 waves per block from 4096 rows
+    # 8192 rows of 2048 fill one resident round at 8 rows per wave: 256 blocks of 4 waves
+    ("add_rmsnorm_8192x2048", "headline", "k_rmsnorm_rowsILi8ELb1EE", 256 * 256, 134221824),
+    # 8192 blocks of 256 threads over 2,097,152 vectors; the scatters: one row per wave, 4 waves
+    # per block from 4096 rows
     ("residual_add_8192x2048", "residual_add", "k_residual_add_vec", 8192 * 256, 100663296),
-    ("rmsnorm_8192x2048", "rmsnorm_8192", "k_rmsnorm_waveILi4ELb0ELb1E", 2048 * 256, 67112960),
+    ("rmsnorm_8192x2048", "rmsnorm_8192", "k_rmsnorm_rowsILi8ELb0EE", 256 * 256, 67112960),
     ("kv_scatter_8192", "kv_scatter_8192", "k_kv_scatterILb0ELi1E", 2048 * 256, 16779264),
     ("kv_scatter_batch_256", "kv_scatter_batch_256", "k_kv_scatterILb1ELi1E", 256 * 64, 526336),
     ("rmsnorm_16x2048", "rmsnorm_16", "k_rmsnorm_waveILi4ELb0ELb1E", 16 * 64, 135168),
