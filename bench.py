@@ -39,8 +39,10 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import glob
 import json
 import os
+import re
 import sys
 import time
 
@@ -1662,8 +1664,23 @@ def summary(kernels: dict, torch, dev, K: int, W: int) -> None:
     """The run's headline figures, a few lines at the very end of stderr (a reader that keeps
     only the tail of the log still gets every configuration's time and roofline fraction)."""
     p = torch.cuda.get_device_properties(dev)
-    log(f"summary: {p.name} ({getattr(p, 'gcnArchName', '?')}, {p.multi_processor_count} CUs), "
-        f"steps={K} warmup={W}; us = event-timed mean per launch, % of 8 TB/s")
+    # The HBM vendor and the top shader clock level, from the amdgpu driver's sysfs (boxes of
+    # the same model differ in both; unreadable entries are left out).
+    box = []
+    for name, pick in (("mem_info_vram_vendor", lambda t: f"HBM {t.strip()}"),
+                       ("pp_dpm_sclk", lambda t: "sclk up to %d MHz" % max(
+                           int(m) for m in re.findall(r"(\d+)\s*[Mm][Hh]z", t)))):
+        vals = set()
+        for f in sorted(glob.glob(f"/sys/class/drm/card*/device/{name}")):
+            try:
+                with open(f) as fh:
+                    vals.add(pick(fh.read()))
+            except (OSError, ValueError):
+                pass
+        box += sorted(vals)
+    log(f"summary: {p.name} ({getattr(p, 'gcnArchName', '?')}, {p.multi_processor_count} CUs"
+        f"{', ' + ', '.join(box) if box else ''}), steps={K} warmup={W}; us = event-timed mean "
+        f"per launch, % of 8 TB/s")
     rows = [("config 2 add+RMSNorm [8192,2048]", "add_rmsnorm_8192x2048"),
             ("config 3 RoPE 8192 tokens", "rope_8192"),
             ("config 4a SwiGLU [8192,8192]", "swiglu_8192x8192"),
