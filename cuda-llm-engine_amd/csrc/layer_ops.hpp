@@ -295,6 +295,10 @@ __device__ __forceinline__ void rope_tile(
 // rather than once for every element slot some lane needs it in.
 template <int NV>
 __device__ __forceinline__ void silu_vectors(const u32x4 (&g)[NV], u32x4 (&s)[NV]) {
+  // One bit per element: 4 vectors of 8 at most. A wider shift of the 32-bit mask is undefined,
+  // and the compiler then drops the code that follows (8 vectors per lane lost every
+  // v_exp_f32 of the kernel, whose waves ran past its end).
+  static_assert(NV >= 1 && NV <= 4, "the pending mask holds 32 elements");
   uint32_t pending = 0;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
