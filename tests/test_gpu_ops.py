@@ -196,6 +196,10 @@ def test_norms_of_many_rows_give_the_bits_of_one_row_per_wave(llmk, rows):
     got = host(o1)
     assert np.array_equal(got[:rows * hidden], host(o2)), f"add_rmsnorm {rows} rows"
     assert np.all(got[rows * hidden:] == CANARY)
+    # in place (out == x): each wave reads all of its rows before it writes any
+    dx2 = dx.clone()
+    llmk.rmsnorm(dx2, dw, dx2, rows, hidden, EPS)
+    assert np.array_equal(host(dx2), host(whole)[:rows * hidden]), f"in place {rows} rows"
 
 
 def test_add_rmsnorm_equals_residual_add_then_rmsnorm(llmk):
