@@ -954,7 +954,12 @@ int attn_launch(const AttnArgs& a, hipStream_t s) {
   const int pps = (a.max_pages + a.num_splits - 1) / a.num_splits;  // pages per split
   const bool short_runs = a.part_o && a.num_splits >= 3 && pps <= kShortRunPages &&
                           (long long)a.n_seq * groups <= kSplitGridPairs;
-  if (a.num_splits >= 3 && a.part_o && !short_runs) {
+  // The page-balanced kernel counts the batch's units in 32-bit ints: at most
+  // n_seq * (start_units + max_pages) of them. Batches that could exceed that take the
+  // sequence-split grid, which needs no count.
+  const bool units_fit =
+      (long long)a.n_seq * (start_units<KVW>() + (long long)a.max_pages) <= 0x7FFFFFFFLL;
+  if (a.num_splits >= 3 && a.part_o && !short_runs && units_fit) {
     int blocks = balanced_blocks() / groups;
     if (blocks < 1) blocks = 1;
     int st = launch(k_attn_balanced<KVW>, dim3((unsigned)blocks, (unsigned)groups), dim3(kThreads),
