@@ -170,11 +170,11 @@ PROFILE_SHAPES = [
     # the pass with one launch per layer: 256 norm rows, 256 RoPE tokens, 4096 SwiGLU chunks
     ("decode_layers:layer_256", "pass_layers", "k_layer_passILi4ELb0ELi6ELb0E|k_layer_pass<4, false, 6, false>",
      4608 * 64, 4198400 + 3147904 + 12582912),
-    # the whole pass in one launch: 256 residual chains, 16 x 256 RoPE tokens, 16 x 4096 SwiGLU
-    # chunks; bytes: what it must move (config 5's count less the residual rows it keeps in
-    # registers, workloads.bytes_decode_pass_fused)
+    # the whole pass in one launch: 256 residual chains, 16 x 256 RoPE tokens, 16 x 2048 SwiGLU
+    # chunks of two vectors per lane; bytes: what it must move (config 5's count less the
+    # residual rows it keeps in registers, workloads.bytes_decode_pass_fused)
     ("decode_fused:pass_256", "pass_fused", "k_layers_fusedILi4ELi6ELb0ELb1E|k_layers_fused<4, 6, false, true>",
-     (256 + 16 * 256 + 16 * 4096) * 64, 303139840),
+     (256 + 16 * 256 + 16 * 2048) * 64, 303139840),
 ]
 
 

@@ -104,6 +104,14 @@ int launch_layer_vpl(const LayerArgs& a, int tasks, unsigned blocks, size_t lds,
 // ---------------------------------------------------------------------------------------------
 constexpr int kFusedLayers = 16;
 
+// Vectors per lane of the one-launch pass's SwiGLU chunks (one-wave blocks). With one norm per
+// layer, two halve the launch's blocks: same box, config 5, bits unchanged, 54.3 us with one,
+// 53.0 with two, 55.5 with four. With both of the layer's norms (longer residual chains) two
+// measured 69.5 us against 59.2 with one. (The stand-alone SwiGLU kernels keep one: there two
+// measured slower.)
+template <bool NORM2>
+constexpr int fused_swiglu_unroll() { return NORM2 ? 1 : 2; }
+
 struct FusedArgs {
   const f16* x[kFusedLayers];
   const f16* norm_w[kFusedLayers];
@@ -217,14 +225,15 @@ __global__ void __launch_bounds__(kWave) k_layers_fused(FusedArgs a) {
                                      nullptr, 0);
     return;
   }
-  constexpr size_t chunk = (size_t)kSwigluThreads * kSwigluUnroll;
+  constexpr int U = fused_swiglu_unroll<NORM2>();
+  constexpr size_t chunk = (size_t)kSwigluThreads * U;
   const int c = r - a.layers * a.n;
   const int l = (int)fdiv((uint32_t)c, a.cdiv);
   const size_t cb = (size_t)(c - l * (int)a.cdiv.d) * chunk;
   if (cb + chunk <= a.swiglu_nvec)
-    swiglu_block<kSwigluUnroll>(a.gate[l], a.up[l], a.act[l], cb, a.swiglu_nvec, true);
+    swiglu_block<U>(a.gate[l], a.up[l], a.act[l], cb, a.swiglu_nvec, true);
   else
-    swiglu_block<kSwigluUnroll>(a.gate[l], a.up[l], a.act[l], cb, a.swiglu_nvec, false);
+    swiglu_block<U>(a.gate[l], a.up[l], a.act[l], cb, a.swiglu_nvec, false);
 }
 
 template <bool STORE_ALL>
@@ -402,8 +411,9 @@ static int fused_pass(const llmk_decode_pass* p, void* stream) {
   a.nkv = p->n_kv_heads;
   a.hidden_f = (float)p->hidden;
   a.eps = p->eps;
-  const size_t chunks = (a.swiglu_nvec + kSwigluThreads * kSwigluUnroll - 1) /
-                        (kSwigluThreads * kSwigluUnroll);
+  const size_t chunk = (size_t)kSwigluThreads *
+                       (two_norms ? fused_swiglu_unroll<true>() : fused_swiglu_unroll<false>());
+  const size_t chunks = (a.swiglu_nvec + chunk - 1) / chunk;
   a.cdiv = make_fastdiv((uint32_t)chunks);
   if ((1 + (size_t)kFusedLayers) * n + kFusedLayers * chunks > 0x7FFFFFFFu)
     return LLMK_ERR_UNSUPPORTED;
