@@ -61,7 +61,8 @@ SECTIONS = ["headline", "rmsnorm_16", "rope_8192", "swiglu_8192", "embedding_819
             "argmax", "step_256", "step_8", "sched", "probe_sweep", "probe_kernels", "copy_1GiB",
             "residual_add", "rmsnorm_8192", "kv_scatter_8192", "kv_scatter_batch_256",
             "pass2_graph", "pass2_layers", "pass_fused", "pass2_fused", "calib", "calib_resident",
-            "calib_hbm", "end", "setup", "sched_ab"]
+            "calib_hbm", "end", "setup", "sched_ab", "pass_fused_eager", "pass2_fused_eager",
+            "pass_layers_eager"]
 
 # Launch shapes (blocks, threads) of the 16-layer pass at 256 sequences, from the launchers'
 # grid rules: the embedding and add+RMSNorm take one 64-thread wave per row below 4096 rows
@@ -906,7 +907,15 @@ class Bench:
             "decode pass, both norms, one launch", nb, t, None,
             {"launches": 1, "layers": L, "seqs": n, "sets": 2, "moved_bytes": moved,
              "moved_frac_of_peak": round(moved / t["mean_s"] / 1e9 / PEAK_GBS, 4)})
-        del fgraphs, dps, ps
+        del fgraphs
+        # a single kernel needs no graph: launched directly, it skips the graph launch's own cost
+        self.mark("pass2_fused_eager")
+        t = self.run(lambda i: dps[i].run_fused(), 2, steps, warm)
+        self.kernels["decode_pass_16x256_two_norms_fused_eager"] = kernel_entry(
+            "decode pass, both norms, one launch (direct)", nb, t, None,
+            {"launches": 1, "layers": L, "seqs": n, "sets": 2, "moved_bytes": moved,
+             "moved_frac_of_peak": round(moved / t["mean_s"] / 1e9 / PEAK_GBS, 4)})
+        del dps, ps
         self.free()
 
     # ------------------------------------------------------------------ config 5
@@ -972,6 +981,11 @@ class Bench:
                      "per-layer inputs are independent, not for a decode step with GEMMs "
                      "between the ops"})
         del lgraphs
+        self.mark("pass_layers_eager")
+        t = self.run(lambda i: dps[i].run_layers(), 2, steps, warm)
+        self.kernels["decode_pass_16x256_layers_eager"] = kernel_entry(
+            "decode pass, one launch per layer (direct)", nb, t, None,
+            {"launches": L, "layers": L, "seqs": n, "sets": 2})
         # the whole pass in one launch (llmk_decode_nongemm_pass_fused): the residual chains of
         # all 16 layers beside every layer's RoPE + scatter tokens and SwiGLU chunks
         fgraphs = [capture(dp.run_fused) for dp in dps]
@@ -988,6 +1002,14 @@ class Bench:
                      "count, `moved_bytes` what this launch must move (no embedding rows "
                      "written and re-read, no residual re-read per layer)"})
         del fgraphs
+        # the same launch made directly, back to back: a graph of one kernel adds the graph
+        # launch's own cost to every pass and saves nothing
+        self.mark("pass_fused_eager")
+        t = self.run(lambda i: dps[i].run_fused(), 2, steps, warm)
+        self.kernels["decode_pass_16x256_fused_eager"] = kernel_entry(
+            "decode pass, one launch (direct)", nb, t, None,
+            {"launches": 1, "layers": L, "seqs": n, "sets": 2, "moved_bytes": moved,
+             "moved_frac_of_peak": round(moved / t["mean_s"] / 1e9 / PEAK_GBS, 4)})
 
         # ---- breakdown
         def stage_fn(op, p):
@@ -1686,9 +1708,12 @@ def summary(kernels: dict, torch, dev, K: int, W: int) -> None:
             ("config 4a SwiGLU [8192,8192]", "swiglu_8192x8192"),
             ("config 4b embedding 8192 ids", "embedding_8192"),
             ("config 1 RMSNorm [16,2048]", "rmsnorm_16x2048"),
-            ("config 5 pass, one launch", "decode_pass_16x256_fused"),
+            ("config 5 pass, one launch", "decode_pass_16x256_fused_eager"),
+            ("config 5 pass, one launch, graph", "decode_pass_16x256_fused"),
             ("config 5 pass, per layer", "decode_pass_16x256_layers"),
-            ("config 5 pass, op by op", "decode_pass_16x256"),
+            ("config 5 pass, per layer, direct", "decode_pass_16x256_layers_eager"),
+            ("config 5 pass, op by op", "decode_pass_16x256_eager"),
+            ("config 5 pass, op by op, graph", "decode_pass_16x256"),
             ("attention 256 of U[1,2048]", "attention_decode_256"),
             ("attention 16 x 2048", "attention_decode_16x2048"),
             ("argmax [256,128256]", "argmax_256x128256"),
