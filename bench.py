@@ -1503,6 +1503,63 @@ class Bench:
         del graph
         self.free()
         self.kernels[f"decode_step_1b_{n}"] = e
+        if n > llmk.LINEAR_ROWS_MAX:  # the projections are hipBLASLt calls: time a C++ caller too
+            c = self.decode_step_cpp(cfg, tokens, pos, tables, used, 128, nbytes,
+                                     max(20, self.K // 4), max(5, self.W // 4))
+            if c:
+                self.kernels[f"decode_step_1b_{n}_cpp"] = c
+
+    def decode_step_cpp(self, cfg, tokens, pos, tables, used, max_pages, nbytes, steps, warm):
+        """The same step timed by llmk_step_bench, a C++ process linking the library: there
+        libllmk's hipBLASLt and HIP runtime are the system's, as for any C/C++ caller, while in
+        this process they are the copies torch loaded. Same config and rows (written to a file
+        for it), weights and pools of the same distributions; graph launches timed back to back
+        with HIP events."""
+        import subprocess
+        import tempfile
+        np = self.np
+        exe = os.path.join(ROOT, "cuda-llm-engine_amd", "llmk_step_bench")
+        if not os.path.exists(exe):
+            log("  decode step from C++: llmk_step_bench is not built; skipped")
+            return None
+        if os.environ.get("ROCPROF_OUTPUT_PATH"):  # set by rocprofv3 for the program it traces
+            # Traced by rocprofv3, llmk_step_bench ended in a host segmentation fault inside the
+            # HIP runtime, below llmk_engine_forward_graph; untraced it runs to the end.
+            log("  decode step from C++: skipped under rocprofv3")
+            return None
+        tok = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        n = tok.size
+        tab = np.asarray(tables, np.int32).reshape(n, -1)[:, :max_pages]
+        tab = np.ascontiguousarray(np.pad(tab, ((0, 0), (0, max_pages - tab.shape[1]))))
+        fd, path = tempfile.mkstemp(suffix=".rows")
+        try:
+            with os.fdopen(fd, "wb") as f:
+                f.write(b"LLMKROWS")
+                f.write(bytes(cfg))
+                f.write(np.array([n, max_pages, used], np.int32).tobytes())
+                f.write(tok.tobytes())
+                f.write(np.ascontiguousarray(pos, np.int32).reshape(-1).tobytes())
+                f.write(tab.tobytes())
+            r = subprocess.run([exe, path, str(steps), str(warm)], capture_output=True,
+                               text=True, timeout=300)
+        finally:
+            os.unlink(path)
+        if r.returncode != 0:
+            log(f"  decode step from C++: llmk_step_bench exited with {r.returncode}: "
+                f"{r.stderr.strip()[-300:]}")
+            return None
+        d = json.loads(r.stdout.strip().splitlines()[-1])
+        mean_s = d["us_mean"] * 1e-6
+        t = {"mean_s": mean_s, "wall_s": mean_s * d["steps"], "steps": d["steps"],
+             "queue_prefilled": False}
+        e = kernel_entry(f"decode step 1B, {n} seqs, C++ caller (graph)", nbytes, t, None, {
+            "tokens_per_s": round(n / mean_s, 1), "seqs": int(n), "steps": d["steps"],
+            "hipblaslt": d["hipblaslt"], "amdhip64": d["amdhip64"],
+            "note": "the same step from llmk_step_bench, a C++ process: the system's hipBLASLt "
+                    "and HIP runtime, as any C/C++ caller of the library gets them (this Python "
+                    "process uses the copies torch loaded)"})
+        log(f"    -> {e['tokens_per_s']:.0f} tokens/s with {d['hipblaslt']}")
+        return e
 
     def scheduler(self):
         """The reference's scheduler benchmark on the engine (Llama-3.2-1B shape, seeded random
@@ -1720,6 +1777,7 @@ def summary(kernels: dict, torch, dev, K: int, W: int) -> None:
             ("residual add [8192,2048]", "residual_add_8192x2048"),
             ("RMSNorm [8192,2048]", "rmsnorm_8192x2048"),
             ("decode step 1B, 256 rows", "decode_step_1b_256"),
+            ("decode step 1B, 256 rows, from C++", "decode_step_1b_256_cpp"),
             ("decode step 1B, 8 rows", "decode_step_1b_8"),
             ("copy probe 1 GiB", "copy_1GiB")]
     for label, key in rows:
