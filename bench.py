@@ -631,6 +631,27 @@ def kernel_entry(name, nbytes, t, traffic=None, extra=None):
     return e
 
 
+def write_step_rows(path, cfg, tokens, positions, tables, num_pages, max_pages) -> None:
+    """The rows file llmk_step_bench reads (csrc/step_bench.hip): b"LLMKROWS", the
+    llmk_model_config struct (`cfg`, a ctypes mirror of it), int32 n_rows, max_pages, num_pages,
+    then int32 tokens[n], positions[n] and block_tables[n, max_pages] (zero-padded)."""
+    import numpy as np
+    tok = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+    n = tok.size
+    pos = np.ascontiguousarray(positions, np.int32).reshape(-1)
+    if pos.size != n:
+        raise ValueError("tokens and positions differ in length")
+    tab = np.asarray(tables, np.int32).reshape(n, -1)[:, :max_pages]
+    tab = np.ascontiguousarray(np.pad(tab, ((0, 0), (0, max_pages - tab.shape[1]))))
+    with open(path, "wb") as f:
+        f.write(b"LLMKROWS")
+        f.write(bytes(cfg))
+        f.write(np.array([n, max_pages, num_pages], np.int32).tobytes())
+        f.write(tok.tobytes())
+        f.write(pos.tobytes())
+        f.write(tab.tobytes())
+
+
 def sets_for(bytes_per_set: int, floor: int = 1 << 30, most: int = 64) -> int:
     return max(2, min(most, -(-floor // max(1, bytes_per_set)) + 1))
 
@@ -1527,19 +1548,11 @@ class Bench:
             # HIP runtime, below llmk_engine_forward_graph; untraced it runs to the end.
             log("  decode step from C++: skipped under rocprofv3")
             return None
-        tok = np.ascontiguousarray(tokens, np.int32).reshape(-1)
-        n = tok.size
-        tab = np.asarray(tables, np.int32).reshape(n, -1)[:, :max_pages]
-        tab = np.ascontiguousarray(np.pad(tab, ((0, 0), (0, max_pages - tab.shape[1]))))
+        n = np.asarray(tokens).size
         fd, path = tempfile.mkstemp(suffix=".rows")
+        os.close(fd)
         try:
-            with os.fdopen(fd, "wb") as f:
-                f.write(b"LLMKROWS")
-                f.write(bytes(cfg))
-                f.write(np.array([n, max_pages, used], np.int32).tobytes())
-                f.write(tok.tobytes())
-                f.write(np.ascontiguousarray(pos, np.int32).reshape(-1).tobytes())
-                f.write(tab.tobytes())
+            write_step_rows(path, cfg, tokens, pos, tables, used, max_pages)
             r = subprocess.run([exe, path, str(steps), str(warm)], capture_output=True,
                                text=True, timeout=300)
         finally:
