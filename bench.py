@@ -1555,6 +1555,9 @@ class Bench:
             write_step_rows(path, cfg, tokens, pos, tables, used, max_pages)
             r = subprocess.run([exe, path, str(steps), str(warm)], capture_output=True,
                                text=True, timeout=300)
+        except subprocess.TimeoutExpired:
+            log("  decode step from C++: llmk_step_bench did not finish in 300 s; skipped")
+            return None
         finally:
             os.unlink(path)
         if r.returncode != 0:
